@@ -1,0 +1,370 @@
+"""Benchmark of the MI355X sparse expert reader (one JSON line on stdout).
+
+Workload (`--config`, default c2): the BASELINE configuration the metric is
+quoted on that fits one GPU -- a stack of L distinct synthetic MoE layers
+(random-init BF16 weights, their ternary sketches and rank-32 recovery maps),
+each with its own decode batch of T tokens routed by a softmax router. One
+step replays a HIP graph holding the L reader calls on one stream; the reported
+value is microseconds per layer (mean over the timed steps).
+
+Also reported: tokens/s, the algorithmic HBM bytes of each layer call (per
+expert touched: union of kept coordinates' code runs, FP16 scale plane and FP32
+norms, union of kept channels' gate/up and down rows, union of skipped
+channels' encoder rows; plus U, signs, inputs and outputs), the achieved GB/s,
+a live per-stage kernel timing whose dominant stage gives the roofline object,
+and the CPU oracle on the C1 layer as the CPU baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "calibration-free-moe_amd"), ROOT]
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+from calibration_free_moe.reader import _ext  # noqa: E402
+from calibration_free_moe.reader.budget import compile_budget  # noqa: E402
+from calibration_free_moe.reader.progressive import (  # noqa: E402
+    ProgressiveReader,
+    ReaderWorkspace,
+    channel_major_down,
+)
+from calibration_free_moe.reader.sketch import block_hadamard_signs, build_sketch  # noqa: E402
+
+METRIC = "sparse MoE-layer decode µs/layer at batch 1/64/128; achieved HBM GB/s on bytes read"
+HBM_PEAK_GBPS = 8000.0
+
+CONFIGS = {
+    # name: (hidden, width, experts, top_k, layers, tokens, retention, keep, description)
+    "c1": (2048, 1024, 64, 8, 1, 1, 0.123, 0.625, "OLMoE-1B-7B layer, batch 1"),
+    "c2": (2048, 1024, 64, 8, 16, 64, 0.123, 0.625, "OLMoE-1B-7B layer x16, batch 64"),
+    "c3": (2048, 768, 128, 8, 48, 1, 0.123, 0.625, "Qwen3-30B-A3B layer x48"),
+    "c5": (2048, 512, 256, 8, 16, 1, 0.123, 0.625, "256-expert I=512 layer x16"),
+}
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def device_weights(hidden, width, experts, rank, seed, device, std=0.02):
+    """One synthetic layer's weights, generated on the GPU (recipe of tests/synthetic.py)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    gate_up = (torch.randn(experts, 2 * width, hidden, generator=g, device=device) * std).bfloat16()
+    down = (torch.randn(experts, hidden, width, generator=g, device=device) * std).bfloat16()
+    router = (torch.randn(experts, hidden, generator=g, device=device) * std).bfloat16()
+    gram = torch.einsum("ehi,egi->hg", down.float(), down.float())
+    try:
+        _, vectors = torch.linalg.eigh(gram.double())
+    except RuntimeError:
+        _, vectors = torch.linalg.eigh(gram.double().cpu())
+    u = vectors[:, -rank:].flip(-1).float().to(device)
+    encoder = torch.einsum("hr,ehi->eri", u, down.float()).bfloat16()
+    decoder = u.bfloat16().contiguous()
+    codes, stats = build_sketch(gate_up, block_hadamard_signs(hidden, device))
+    return {
+        "gate_up": gate_up, "down": channel_major_down(down), "encoder": encoder,
+        "decoder": decoder, "sketch": (codes, stats), "router": router,
+    }
+
+
+def device_inputs(weights, tokens, top_k, seed, device):
+    """A routed decode batch: N(0, 1) states with 1 % of dims x20, softmax top-k."""
+    hidden = weights["router"].shape[1]
+    g = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(tokens, hidden, generator=g, device=device)
+    dims = torch.randperm(hidden, generator=g, device=device)[: max(1, round(0.01 * hidden))]
+    x[:, dims] *= 20
+    x = x.bfloat16()
+    logits = (x.float() @ weights["router"].float().T).bfloat16().float()
+    probabilities, ids = torch.softmax(logits, -1).topk(top_k, -1)
+    probabilities = (probabilities / probabilities.sum(-1, keepdim=True)).float().contiguous()
+    return {"hidden": x, "ids": ids.to(torch.int64).contiguous(), "weights": probabilities,
+            "out": torch.empty_like(x)}
+
+
+def device_layer(hidden, width, experts, top_k, rank, tokens, seed, device):
+    data = device_weights(hidden, width, experts, rank, seed, device)
+    data.update(device_inputs(data, tokens, top_k, seed + 7, device))
+    return data
+
+
+def algorithmic_bytes(reader: ProgressiveReader, tokens: int) -> dict[str, int]:
+    """Bytes one call must read: per-expert unions over the batch (host count)."""
+    p = reader.plan
+    h, i, k = p.hidden_size, p.expert_width, p.top_k
+    blocks = h // 128
+    rank = reader.rank
+    ids = reader.ids[:tokens].cpu().numpy()
+    selected = reader.selected[:tokens].cpu().numpy().reshape(tokens, k, i).astype(bool)
+    keep = p.screen_coordinates
+    coords = (reader.sketch_coordinates[:tokens].cpu().numpy() if keep < 128
+              else np.broadcast_to(np.arange(128), (tokens, blocks, 128)))
+    run = 32 * -(-2 * ((i + 4) // 5) // 32)
+    planes = 1 + (reader.selection_score != "point")
+    totals = {"sketch": 0, "gate_up": 0, "down": 0, "encoder": 0, "fixed": 0}
+    for expert in np.unique(ids):
+        rows = np.argwhere(ids == expert)
+        union_coords = 0
+        for b in range(blocks):
+            union_coords += len(np.unique(coords[rows[:, 0], b].reshape(-1)))
+        totals["sketch"] += union_coords * run + blocks * 2 * i * 2 * planes + 4 * i
+        kept = np.zeros(i, bool)
+        skipped = np.zeros(i, bool)
+        for t, slot in rows:
+            kept |= selected[t, slot]
+            skipped |= ~selected[t, slot]
+        totals["gate_up"] += int(kept.sum()) * 4 * h
+        totals["down"] += int(kept.sum()) * 2 * h
+        totals["encoder"] += int(skipped.sum()) * 2 * rank
+    totals["fixed"] = 2 * h * rank + h + tokens * (2 * h + 2 * h + 8 * k)
+    totals["total"] = sum(totals.values())
+    return totals
+
+
+STAGE_BYTES = {"screen": ("sketch",), "exact": ("gate_up",), "down": ("down",),
+               "encode": ("encoder",)}
+
+
+def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> tuple[float, list[float]]:
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    events = []
+    for _ in range(steps):
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        graph.replay()
+        end.record()
+        events.append((begin, end))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    return elapsed * 1e3 / steps, [b.elapsed_time(e) for b, e in events]
+
+
+_WEIGHT_CACHE: dict[str, list] = {}
+
+
+def layer_weights(name: str, layers: int, device) -> list:
+    h, i, e, k, _, _, _, _, _ = CONFIGS[name]
+    cached = _WEIGHT_CACHE.get(name)
+    if cached is None or len(cached) != layers:
+        _WEIGHT_CACHE.clear()
+        torch.cuda.empty_cache()
+        started = time.perf_counter()
+        cached = [device_weights(h, i, e, 32, seed=1000 * int(name[1:]) + layer, device=device)
+                  for layer in range(layers)]
+        torch.cuda.synchronize()
+        log(f"[{name}] generated {layers} layers in {time.perf_counter() - started:.1f}s")
+        _WEIGHT_CACHE[name] = cached
+    return cached
+
+
+def run_config(name: str, args, device) -> dict:
+    h, i, e, k, layers, tokens, retention, keep, description = CONFIGS[name]
+    layers = args.layers or layers
+    tokens = args.tokens or tokens
+    rank = 32
+    plan = compile_budget(hidden_size=h, expert_width=i, top_k=k, retention=retention,
+                          screen_keep=keep)
+    log(f"[{name}] {layers} layers (H={h} I={i} E={e} K={k}) batch {tokens}")
+    weights = layer_weights(name, layers, device)
+    workspace = ReaderWorkspace(plan, e, rank, tokens, device)
+    stack = []
+    for layer, w in enumerate(weights):
+        reader = ProgressiveReader(
+            w["gate_up"], w["down"], w["encoder"], w["decoder"], plan, tokens,
+            sketch=w["sketch"], selection_score="point", workspace=workspace,
+        )
+        stack.append((reader, device_inputs(w, tokens, k, seed=7919 * layer + tokens, device=device)))
+    torch.cuda.synchronize()
+    for reader, d in stack:
+        reader(d["hidden"], d["ids"], d["weights"], out=d["out"])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for reader, d in stack:
+            reader(d["hidden"], d["ids"], d["weights"], out=d["out"])
+    ms_per_step, samples = time_graph(graph, args.warmup, args.steps)
+    us_per_layer = ms_per_step * 1e3 / layers
+    log(f"[{name}] {us_per_layer:.2f} us/layer ({ms_per_step:.3f} ms/step)")
+    # algorithmic bytes of each layer call, from that layer's own routes and selections
+    byte_rows = []
+    for reader, d in stack:
+        reader(d["hidden"], d["ids"], d["weights"], out=d["out"])
+        torch.cuda.synchronize()
+        byte_rows.append(algorithmic_bytes(reader, tokens))
+    mean_bytes = {key: float(np.mean([row[key] for row in byte_rows])) for key in byte_rows[0]}
+    # live per-stage timing: each stage relaunched over the whole stack in a graph
+    stage_us = {}
+    repeats = 4
+    for stage in _ext.STAGES:
+        stage_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(stage_graph):
+            for _ in range(repeats):
+                for reader, d in stack:
+                    reader.launch_stage(stage, d["hidden"], d["ids"], d["weights"], None, d["out"])
+        stage_graph.replay()
+        torch.cuda.synchronize()
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        stage_graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        stage_us[stage] = begin.elapsed_time(end) * 1e3 / (repeats * layers)
+    dominant = max(STAGE_BYTES, key=lambda s: stage_us[s])
+    dominant_bytes = sum(mean_bytes[key] for key in STAGE_BYTES[dominant])
+    achieved = dominant_bytes / (stage_us[dominant] * 1e-6) / 1e9
+    return {
+        "name": name,
+        "description": description,
+        "layers": layers,
+        "tokens": tokens,
+        "final_count": plan.final_count,
+        "ms_per_step": ms_per_step,
+        "us_per_layer": us_per_layer,
+        "us_per_layer_median_event": statistics.median(samples) * 1e3 / layers,
+        "tokens_per_s": tokens * 1e6 / (us_per_layer * layers),
+        "layer_tokens_per_s": tokens * 1e6 / us_per_layer,
+        "bytes_per_layer": mean_bytes,
+        "achieved_gbps": mean_bytes["total"] / (us_per_layer * 1e-6) / 1e9,
+        "layer_roofline_frac": mean_bytes["total"] / (us_per_layer * 1e-6) / 1e9 / HBM_PEAK_GBPS,
+        "stage_us": stage_us,
+        "dominant": dominant,
+        "dominant_bytes": dominant_bytes,
+        "dominant_gbps": achieved,
+    }
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The CPU oracle (C, one thread) on the C1 layer: OLMoE shape, batch 1."""
+    from oracle import oracle
+    from tests.synthetic import bits
+
+    h, i, e, k = 2048, 1024, 64, 8
+    plan = compile_budget(hidden_size=h, expert_width=i, top_k=k, retention=0.123,
+                          screen_keep=0.625)
+    data = device_layer(h, i, e, k, 32, 1, seed=1000 * 1, device=torch.device("cuda:0"))
+    codes, stats = data["sketch"]
+    down = data["down"]
+    weights = oracle.Weights(
+        gate_up=bits(data["gate_up"]),
+        down=bits(down.transpose(1, 2)),
+        codes=codes.cpu().contiguous().numpy(),
+        stats=bits(stats.permute(0, 2, 3, 1).contiguous()),
+        norms=down.float().square().sum(1).sqrt().cpu().contiguous().numpy(),
+        signs=block_hadamard_signs(h, "cpu").numpy(),
+        encoder_t=bits(data["encoder"].transpose(1, 2).contiguous()),
+        decoder=bits(data["decoder"]),
+    )
+    x = bits(data["hidden"])
+    ids = data["ids"].cpu().numpy()
+    w = data["weights"].cpu().numpy()
+    runs = []
+    for _ in range(2):
+        oracle.forward(weights, x, ids, w, final_count=plan.final_count, keep=80)
+    deadline = time.perf_counter() + seconds
+    while time.perf_counter() < deadline or len(runs) < 10:
+        begin = time.perf_counter()
+        oracle.forward(weights, x, ids, w, final_count=plan.final_count, keep=80)
+        runs.append(time.perf_counter() - begin)
+    return {
+        "value": statistics.median(runs) * 1e6,
+        "unit": "us/layer",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"C1 OLMoE-shaped layer, batch 1, median of {len(runs)} oracle calls",
+        "gbps_on_algorithmic_bytes": 17_804_352 / statistics.median(runs) / 1e9,
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=4)
+    parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    parser.add_argument("--layers", type=int, default=0)
+    parser.add_argument("--tokens", type=int, default=0)
+    parser.add_argument("--extra", default="c3:1,c3:128",
+                        help="comma list of config:tokens measured beside the headline")
+    parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this reader runs without collectives; got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    device = torch.device("cuda:0")
+    _ext.library()
+    headline = run_config(args.config, args, device)
+    extras = []
+    for item in filter(None, args.extra.split(",")):
+        name, _, count = item.partition(":")
+        sub = argparse.Namespace(**vars(args))
+        sub.layers = 0
+        sub.tokens = int(count) if count else 0
+        torch.cuda.empty_cache()
+        extras.append(run_config(name, sub, device))
+    baseline = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
+    h, i, e, k, layers, tokens, retention, keep, description = CONFIGS[args.config]
+    line = {
+        "metric": METRIC,
+        "value": round(headline["us_per_layer"], 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(headline["ms_per_step"], 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init BF16 weights, seeded router and hidden states)",
+        "config": {
+            "workload": f"{args.config}: {description}",
+            "hidden": h, "expert_width": i, "experts": e, "top_k": k,
+            "layers": headline["layers"], "batch": headline["tokens"],
+            "retention": retention, "screen_keep": keep, "rank": 32,
+            "selection_score": "point", "final_count": headline["final_count"],
+        },
+        "tokens_per_s": round(headline["tokens_per_s"], 1),
+        "achieved_gbps": round(headline["achieved_gbps"], 1),
+        "algorithmic_bytes_per_layer": headline["bytes_per_layer"],
+        "stage_us": {s: round(v, 3) for s, v in headline["stage_us"].items()},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"{headline['dominant']}_kernel",
+            "achieved": round(headline["dominant_gbps"], 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(headline["dominant_gbps"] / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "layer_frac": round(headline["layer_roofline_frac"], 4),
+        },
+        "cpu_baseline": baseline,
+        "extra": [
+            {key: (round(v, 3) if isinstance(v, float) else v) for key, v in x.items()
+             if key in ("name", "description", "layers", "tokens", "us_per_layer",
+                        "tokens_per_s", "achieved_gbps", "layer_roofline_frac", "dominant",
+                        "dominant_gbps", "stage_us")}
+            for x in extras
+        ],
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

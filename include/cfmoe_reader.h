@@ -1,0 +1,158 @@
+/*
+ * C ABI of the MI355X sparse expert reader (libcfmoe_reader.so).
+ *
+ * Plain C: device pointers and sizes only, no framework types. Every call is
+ * stream-ordered on the given HIP stream, never synchronises the host, never
+ * allocates and never frees, so a caller may capture it in a HIP graph. The
+ * caller owns every buffer (weights, workspace, inputs, outputs).
+ *
+ * It replaces the Triton launches of the reference operator
+ * calibration_free_moe/reader/progressive.py (AidenGeunGeun/
+ * calibration-free-moe): ProgressiveReader.__call__ (progressive.py:3876-4472)
+ * maps to cfmoe_forward and ProgressiveReader.prepare_input
+ * (progressive.py:3829-3873) to cfmoe_prepare_input. The Python operator
+ * (calibration_free_moe/reader/progressive.py in this package) keeps the
+ * reference's constructor, call signature, attributes and report() and calls
+ * these entry points through ctypes.
+ *
+ * Return value: 0 on success; otherwise a nonzero code and a message readable
+ * through cfmoe_last_error() (thread-local). Contract violations that the
+ * Python layer already rejects with ValueError return CFMOE_EINVAL here.
+ */
+#ifndef CFMOE_READER_H
+#define CFMOE_READER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *cfmoe_stream;
+
+#define CFMOE_ABI_VERSION 1
+
+/* cfmoe_dims.flags */
+#define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
+#define CFMOE_GELU 2u           /* tanh-GELU gate activation (else SiLU) */
+#define CFMOE_GEOMETRY 4u       /* recovery geometry (alpha, beta) is read */
+#define CFMOE_THRESHOLD 8u      /* keep scores >= *threshold, at most F */
+#define CFMOE_ACCOUNT 16u       /* add fixed per-token read charges */
+#define CFMOE_IDS_INT64 32u     /* router ids are int64 (else int32) */
+#define CFMOE_WEIGHTS_BF16 64u  /* router weights are bf16 (else fp32) */
+#define CFMOE_INPUT_PREPARED 128u /* cfmoe_prepare_input already rotated */
+
+/* Stages of one call, in launch order (cfmoe_launch_stage). */
+#define CFMOE_STAGE_PREPARE 0 /* route, rotate, mask, grid quantisation */
+#define CFMOE_STAGE_SCREEN 1  /* sketch projections per block split */
+#define CFMOE_STAGE_SCORE 2   /* split sums and channel scores */
+#define CFMOE_STAGE_SELECT 3  /* per-token top-F */
+#define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels */
+#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels */
+#define CFMOE_STAGE_DOWN 6    /* down rows of kept channels */
+#define CFMOE_STAGE_OUTPUT 7  /* latent, decoder correction, router mix */
+#define CFMOE_STAGE_COUNT 8
+
+#define CFMOE_EINVAL 1
+#define CFMOE_EHIP 2
+
+/* Layer and plan dimensions (progressive.py:3133-3515 validates the same). */
+typedef struct cfmoe_dims {
+  int32_t hidden;      /* H, multiple of 128 */
+  int32_t width;       /* I, multiple of 16 */
+  int32_t top_k;       /* K <= 64 */
+  int32_t experts;     /* E local experts */
+  int32_t rank;        /* R recovery rank, 0 = no recovery map, <= 64 */
+  int32_t final_count; /* F, channels kept per token */
+  int32_t keep;        /* rotated coordinates kept per 128-block (1..128) */
+  uint32_t flags;
+} cfmoe_dims;
+
+/* Resident per-layer tensors. The reader borrows them; none is written. */
+typedef struct cfmoe_weights {
+  const void *gate_up;     /* bf16 [E, 2I, H] */
+  const void *down;        /* bf16, physical [E, I, H] (channel-major) */
+  const uint8_t *codes;    /* [E, sketch_storage_bytes(2I, H)] */
+  const void *statistics;  /* fp16, physical [E, H/128, 2, 2I] */
+  const float *norms;      /* [E, I] down-column L2 norms */
+  const float *geometry;   /* [E, I, 2] (alpha, beta) or NULL */
+  const void *encoder_t;   /* bf16 [E, I, R] or NULL */
+  const void *decoder;     /* bf16 [H, R] or NULL */
+  const int8_t *signs;     /* [H] rotation signs */
+  const float *threshold;  /* [1] selection threshold or NULL */
+} cfmoe_weights;
+
+/* Caller-allocated scratch, sized for `capacity` tokens (sizes in bytes from
+ * cfmoe_workspace_sizes). Layouts match the reference workspace
+ * (progressive.py:2868-3121) where the Python operator exposes them. */
+typedef struct cfmoe_workspace {
+  int32_t capacity;
+  int32_t *ids;               /* [cap, K] sorted local expert ids */
+  float *weights;             /* [cap, K] router weights in id order */
+  float *planes;              /* [cap, B, keep] kept rotated values */
+  int32_t *coordinates;       /* [cap, B, keep] their coordinates */
+  int32_t *qvals;             /* [cap, B, keep] values on the 21-bit grid */
+  int32_t *qexp;              /* [cap, B] grid exponents */
+  float *norm2;               /* [cap, B] squared norm of kept values */
+  float *partial;             /* [cap, 2, N] gate/up projections */
+  float *variances;           /* [cap, 2, N] */
+  float *screen_parts;        /* [cap, S, 2, N] split partial projections */
+  float *screen_variance_parts; /* [cap, S, 2, N] */
+  float *scores;              /* [cap, N] */
+  int32_t *next_ids;          /* [cap, F] kept candidate ids, ascending */
+  uint8_t *selected;          /* [cap, N] */
+  uint8_t *completed;         /* [cap, N] */
+  void *activations;          /* bf16 [cap, N] */
+  int32_t *starts;            /* [cap, K] */
+  int32_t *counts;            /* [cap, K] */
+  int32_t *tile_starts;       /* [cap, K] 128-channel tiles */
+  int32_t *down_tile_starts;  /* [cap, K] 16-channel tiles */
+  float *down_parts;          /* [cap, F/16 + K, H] */
+  float *encoder_parts;       /* [cap, K, ceil(I/64), R] */
+  float *latent;              /* [cap, R] */
+  double *read_work;          /* [20] read statistics (progressive.py:3507-3515) */
+} cfmoe_workspace;
+
+/* Byte sizes of every workspace buffer, in struct order after `capacity`
+ * (23 entries). Returns the number written. */
+int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
+                          int32_t count);
+
+/* One reader call: routed-expert output of `tokens` rows (progressive.py:
+ * 3876-4472). hidden bf16 [T, H]; router_ids [T, K] int32/int64; router
+ * weights [T, K] fp32/bf16; padding uint8 [T] or NULL; out bf16 [T, H].
+ * charges: 18 doubles added to read_work[0..17] per active token when
+ * CFMOE_ACCOUNT is set (progressive.py:4492-4524), else ignored. */
+int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights,
+                  const cfmoe_workspace *workspace, const void *hidden,
+                  const void *router_ids, const void *router_weights,
+                  const uint8_t *padding, void *out, int32_t tokens,
+                  const double *charges, cfmoe_stream stream);
+
+/* Launch one stage of cfmoe_forward with the same arguments, reading the
+ * workspace state that earlier stages left. For per-kernel timing and tests;
+ * no reference counterpart (the reference launches its Triton kernels
+ * individually from Python, progressive.py:3955-4471). */
+int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weights *weights,
+                       const cfmoe_workspace *workspace, const void *hidden,
+                       const void *router_ids, const void *router_weights,
+                       const uint8_t *padding, void *out, int32_t tokens,
+                       const double *charges, cfmoe_stream stream);
+
+/* Routing-independent input rotation ahead of the router
+ * (progressive.py:3829-3873). A following cfmoe_forward with
+ * CFMOE_INPUT_PREPARED set skips its own rotation. */
+int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,
+                        const cfmoe_workspace *workspace, const void *hidden,
+                        const uint8_t *padding, int32_t tokens, cfmoe_stream stream);
+
+/* Thread-local message of the last failing call. */
+const char *cfmoe_last_error(void);
+
+int cfmoe_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

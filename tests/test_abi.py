@@ -1,0 +1,54 @@
+"""The C-ABI library loads and exports every entry point include/cfmoe_reader.h
+declares (no compute call: this runs without a GPU)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from calibration_free_moe.reader import _ext
+from calibration_free_moe.reader.budget import compile_budget
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "cfmoe_reader.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(cfmoe_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _ext.library()
+    names = declared_functions()
+    assert {"cfmoe_forward", "cfmoe_prepare_input", "cfmoe_launch_stage",
+            "cfmoe_workspace_sizes", "cfmoe_last_error", "cfmoe_abi_version"} <= set(names)
+    for name in names:
+        assert hasattr(lib, name), name
+    assert lib.cfmoe_abi_version() == _ext.ABI_VERSION
+
+
+def test_workspace_sizes_and_contract_errors():
+    plan = compile_budget(hidden_size=2048, expert_width=768, top_k=8, retention=0.123,
+                          screen_keep=0.625)
+    dims = _ext.Dims(2048, 768, 8, 128, 32, plan.final_count, 80, 0)
+    sizes = _ext.workspace_sizes(dims, 4)
+    names = [name for name, _ in _ext.WORKSPACE_FIELDS]
+    assert sizes[names.index("partial")] == 4 * 2 * 6144 * 4
+    assert sizes[names.index("next_ids")] == 4 * plan.final_count * 4
+    bad = _ext.Dims(2000, 768, 8, 128, 32, 10, 80, 0)
+    with pytest.raises(ValueError, match="multiple of 128"):
+        _ext.workspace_sizes(bad, 4)
+
+
+def test_forward_rejects_null_arguments_without_touching_a_device():
+    lib = _ext.library()
+    dims = _ext.Dims(256, 64, 2, 4, 0, 16, 80, 0)
+    weights = _ext.WeightPointers()
+    workspace = _ext.WorkspacePointers()
+    workspace.capacity = 1
+    status = lib.cfmoe_forward(ctypes.byref(dims), ctypes.byref(weights),
+                               ctypes.byref(workspace), None, None, None, None, None, 1,
+                               None, None)
+    assert status == _ext.EINVAL
+    assert b"NULL" in lib.cfmoe_last_error()

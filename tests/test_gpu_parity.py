@@ -1,0 +1,266 @@
+"""HIP reader against the CPU oracle on identical inputs (needs an MI355X).
+
+Every stage is compared bit for bit: routing, rotation, grid values, split
+projections, scores, the selected channel ids, exact activations, latents and
+the BF16 output. Shapes cover the benchmark configurations (OLMoE, Qwen3-30B-
+A3B, the 256-expert I = 512 tail layout) and the reference test suite's edge
+cases (padding rows, all-zero inputs, tied experts, full screen, dense bypass,
+GELU, Gauss-Hermite scores, HIP-graph replay with changing inputs).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from calibration_free_moe.reader.budget import compile_budget
+from calibration_free_moe.reader.progressive import (
+    ProgressiveReader,
+    ReaderWorkspace,
+    channel_major_down,
+)
+from oracle import oracle
+from tests.synthetic import bits, make_layer, oracle_weights
+
+pytestmark = pytest.mark.gpu
+
+DEVICE = torch.device("cuda:0")
+
+
+def build(layer, plan, tokens, **options):
+    return ProgressiveReader(
+        layer.gate_up.to(DEVICE),
+        channel_major_down(layer.down.to(DEVICE)),
+        layer.encoder.to(DEVICE),
+        layer.decoder.to(DEVICE),
+        plan,
+        tokens,
+        sketch=(layer.codes.to(DEVICE), layer.statistics.to(DEVICE)),
+        **options,
+    )
+
+
+def run_both(reader, layer, plan, hidden, ids, weights, padding=None, threshold=None):
+    out = reader(
+        hidden.to(DEVICE), ids.to(DEVICE), weights.to(DEVICE),
+        None if padding is None else padding.to(DEVICE),
+    )
+    torch.cuda.synchronize()
+    expected = oracle.forward(
+        oracle_weights(layer, reader),
+        bits(hidden),
+        ids.cpu().numpy(),
+        weights.cpu().float().numpy(),
+        final_count=plan.final_count,
+        keep=plan.screen_coordinates,
+        padding=None if padding is None else padding.cpu().numpy().astype(np.uint8),
+        point=reader.selection_score == "point",
+        gelu=reader.activation == "gelu_tanh",
+        threshold=threshold,
+    )
+    return out, expected
+
+
+def assert_parity(reader, out, expected, tokens, screened=True):
+    t = tokens
+    got = {
+        "ids": reader.ids[:t].cpu().numpy(),
+        "weights": reader.weights[:t].cpu().numpy(),
+        "selected": reader.selected[:t].cpu().numpy().astype(np.uint8),
+        "next_ids": reader.candidate_ids[-1][:t].cpu().numpy(),
+        "counts": reader.counts[:t].cpu().numpy(),
+        "starts": reader.starts[:t].cpu().numpy(),
+        "tile_starts": reader.tile_starts[:t].cpu().numpy(),
+        "activations": bits(reader.activations[:t]),
+        "completed": reader.completed[:t].cpu().numpy().astype(np.uint8),
+        "partial": reader.partial[:t].cpu().numpy(),
+        "out": bits(out),
+    }
+    if screened:
+        got["planes"] = reader.sketch_planes[:t].cpu().numpy()
+        got["qvals"] = reader.sketch_values[:t].cpu().numpy()
+        got["qexp"] = reader.sketch_exponents[:t].cpu().numpy()
+        got["scores"] = reader.scores[0][:t].cpu().numpy()
+        if reader.plan.screen_coordinates < 128:
+            got["coordinates"] = reader.sketch_coordinates[:t].cpu().numpy()
+    if reader.rank:
+        got["latent"] = reader.latent[:t].cpu().numpy()
+    for name, value in got.items():
+        want = expected[name]
+        if not np.array_equal(value, want):
+            mismatch = np.flatnonzero((value != want).reshape(-1))
+            raise AssertionError(
+                f"{name}: {mismatch.size} of {value.size} differ, first at {mismatch[:5]}"
+            )
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 5])
+@pytest.mark.parametrize("score", ["point", "recovery-aware"])
+def test_small_layer_bit_exact(tokens, score):
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=40 + tokens)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score=score)
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+
+
+def test_padding_zero_input_and_gelu():
+    tokens = 4
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=44)
+    layer.hidden[2] = 0
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.1,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point", activation="gelu_tanh")
+    padding = torch.tensor([False, True, False, False])
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights, padding)
+    assert_parity(reader, out, expected, tokens)
+    assert np.array_equal(expected["next_ids"][2], np.arange(plan.final_count))
+    assert not out[1].float().abs().sum()
+
+
+def test_full_screen_and_bf16_router_weights_int32_ids():
+    tokens = 3
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=45)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.2,
+                          screen_keep=1.0)
+    reader = build(layer, plan, tokens, selection_score="point")
+    weights = layer.weights.bfloat16()
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids.int(), weights)
+    assert_parity(reader, out, expected, tokens)
+
+
+def test_dense_bypass():
+    tokens = 2
+    layer = make_layer(hidden=256, width=64, experts=4, top_k=2, rank=8, tokens=tokens, seed=46)
+    plan = compile_budget(hidden_size=256, expert_width=64, top_k=2, retention=1.0)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens, screened=False)
+
+
+def test_equal_experts_tie_by_expert_id():
+    tokens = 2
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=47)
+    layer.gate_up[1:4] = layer.gate_up[0]
+    layer.down[1:4] = layer.down[0]
+    from calibration_free_moe.reader.sketch import block_hadamard_signs, build_sketch
+    layer.codes, layer.statistics = build_sketch(layer.gate_up, block_hadamard_signs(512, "cpu"))
+    layer.ids[:] = torch.tensor([3, 0, 2, 1])
+    layer.weights[:] = 0.25
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+    scores = reader.scores[0][:tokens].reshape(tokens, 4, 256)
+    assert torch.equal(scores, scores[:, :1].expand_as(scores))
+
+
+def test_threshold_selection():
+    tokens = 3
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=48)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    probe = build(layer, plan, tokens, selection_score="point")
+    probe(layer.hidden.to(DEVICE), layer.ids.to(DEVICE), layer.weights.to(DEVICE))
+    tau = float(probe.scores[0][0].sort(descending=True).values[60])
+    reader = build(layer, plan, tokens, selection_score="point", selection_threshold=tau)
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights,
+                             threshold=tau)
+    assert_parity(reader, out, expected, tokens)
+    assert reader.report()["charged_bytes"] > 0
+
+
+@pytest.mark.parametrize(
+    "hidden,width,experts,top_k,retention,tokens",
+    [
+        (2048, 1024, 64, 8, 0.123, 1),  # OLMoE-1B-7B layer, batch one
+        (2048, 768, 128, 8, 0.123, 1),  # Qwen3-30B-A3B layer, batch one
+        (2048, 768, 128, 8, 0.123, 4),
+        (2048, 512, 256, 8, 0.123, 2),  # 256 experts, I = 512 block-paired tails
+    ],
+)
+def test_benchmark_shapes_bit_exact(hidden, width, experts, top_k, retention, tokens):
+    layer = make_layer(hidden=hidden, width=width, experts=experts, top_k=top_k, rank=32,
+                       tokens=tokens, seed=50 + tokens)
+    plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=top_k,
+                          retention=retention, screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+    report = reader.report()
+    charged = (plan.selected_weight_bytes() + plan.recovery_read_bytes(32)
+               + plan.selection_read_bytes(False) + plan.sketch_read_bytes(False) + hidden)
+    assert report["charged_bytes"] == tokens * charged
+    assert report["reference_bytes"] == tokens * plan.native_read_bytes()
+
+
+def test_graph_replay_with_changing_inputs():
+    tokens = 4
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=60)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    x = layer.hidden.to(DEVICE).clone()
+    ids = layer.ids.to(DEVICE).clone()
+    weights = layer.weights.to(DEVICE).clone()
+    padding = torch.zeros(tokens, dtype=torch.bool, device=DEVICE)
+    out = reader(x, ids, weights, padding)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = reader(x, ids, weights, padding)
+    generator = torch.Generator().manual_seed(3)
+    for replay in range(4):
+        x.copy_(torch.randn(tokens, 512, generator=generator).bfloat16())
+        if replay == 2:
+            x.zero_()
+        padding.zero_()
+        padding[1] = replay % 2 == 1
+        ids.copy_(ids.flip(1))
+        weights.uniform_(0.2, 0.8)
+        reader.read_work.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = oracle.forward(
+            oracle_weights(layer, reader), bits(x), ids.cpu().numpy(),
+            weights.cpu().numpy(), final_count=plan.final_count, keep=80,
+            padding=padding.cpu().numpy().astype(np.uint8),
+        )
+        assert_parity(reader, out, expected, tokens)
+        active = int((~padding).sum())
+        assert reader.report()["reference_bytes"] == active * plan.native_read_bytes()
+
+
+def test_shared_workspace_between_layers():
+    tokens = 3
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    small = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.08,
+                           screen_keep=0.625)
+    first = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=61)
+    second = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=62)
+    workspace = ReaderWorkspace(plan, 8, 16, tokens, DEVICE)
+    a = build(first, plan, tokens, selection_score="point", workspace=workspace)
+    b = build(second, small, tokens, selection_score="point", workspace=workspace)
+    assert a.workspace_bytes > 0 and b.workspace_bytes == 0
+    out_b, expected_b = run_both(b, second, small, second.hidden, second.ids, second.weights)
+    assert_parity(b, out_b, expected_b, tokens)
+    out_a, expected_a = run_both(a, first, plan, first.hidden, first.ids, first.weights)
+    assert_parity(a, out_a, expected_a, tokens)
+
+
+def test_large_batch_selection_is_top_f_of_own_scores():
+    """Batch 64 at the OLMoE shape: size-independent properties plus sampled parity."""
+    tokens = 64
+    layer = make_layer(hidden=2048, width=1024, experts=64, top_k=8, rank=32, tokens=tokens,
+                       seed=70)
+    plan = compile_budget(hidden_size=2048, expert_width=1024, top_k=8, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+    scores = reader.scores[0][:tokens].cpu()
+    order = scores.argsort(dim=1, descending=True, stable=True)[:, : plan.final_count]
+    membership = torch.zeros_like(scores, dtype=torch.bool).scatter_(1, order, True)
+    assert torch.equal(reader.selected[:tokens].cpu(), membership)

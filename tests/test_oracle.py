@@ -1,0 +1,408 @@
+"""Pins of the CPU oracle (oracle/cfmoe_oracle.c) against mathematics and an
+independent float64 restatement of the reference reader.
+
+The float64 restatement follows the reference's own PyTorch references
+(tests/test_progressive_reader.py:102-267: `_reference_screen`,
+`_reference_output`): dense trit * scale projections of the masked rotated
+input, point or Gauss-Hermite scores, a stable top-F, exact BF16 activations,
+per-expert BF16 down sums and the BF16 recovery terms.
+"""
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from calibration_free_moe.reader.budget import compile_budget
+from calibration_free_moe.reader.sketch import (
+    block_hadamard_signs,
+    mask_rotated_blocks,
+    rotate_blocks,
+    unpack_sketch,
+)
+from oracle import oracle
+from tests.synthetic import bits, cpu_weights, make_layer
+
+GH_NODES = (-2.8569700138728056, -1.355626179974266, 0.0, 1.355626179974266,
+            2.8569700138728056)
+GH_WEIGHTS = (0.011257411327720693, 0.2220759220056126, 0.5333333333333333,
+              0.2220759220056126, 0.011257411327720693)
+
+
+def f32(value: float) -> float:
+    return float(np.float32(value))
+
+
+def exact_fmaf(a: float, b: float, c: float) -> float:
+    """Correctly rounded FP32 fma via exact rationals (ties to even)."""
+    value = Fraction(a) * Fraction(b) + Fraction(c)
+    if value == 0:
+        return 0.0
+    low = np.float32(float(value))
+    # float(Fraction) rounds once to float64; fix a possible double rounding.
+    candidates = [np.nextafter(low, np.float32(-np.inf)), low,
+                  np.nextafter(low, np.float32(np.inf))]
+    best = min(candidates, key=lambda v: (abs(Fraction(float(v)) - value),
+                                          int(np.float32(v).view(np.uint32)) & 1))
+    return float(best)
+
+
+# ---------------------------------------------------------------------------
+# scalar functions
+
+
+def test_exp_within_one_ulp():
+    for x in np.linspace(-87.0, 88.0, 4001, dtype=np.float32):
+        got = oracle.expf(float(x))
+        want = math.exp(float(x))
+        assert abs(got - want) <= float(np.spacing(np.float32(want))), x
+    assert oracle.expf(-200.0) == 0.0
+    assert math.isinf(oracle.expf(100.0))
+    assert oracle.expf(0.0) == 1.0
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_activation_matches_torch(gelu):
+    x = torch.linspace(-12, 12, 2001)
+    want = (torch.nn.functional.gelu(x.double(), approximate="tanh") if gelu
+            else torch.nn.functional.silu(x.double()))
+    got = torch.tensor([oracle.activate(float(v), gelu) for v in x], dtype=torch.float64)
+    torch.testing.assert_close(got, want, rtol=3e-6, atol=3e-7)
+
+
+def gh5_reference(g, u, vg, vu, norm, weight, alpha, beta, gelu=False):
+    """Float64 restatement of the recovery-aware score (progressive.py:1304-1353)."""
+    act = (lambda z: z * 0.5 * (1 + math.tanh(0.7978845608028654 * (z + 0.044715 * z**3)))) if gelu \
+        else (lambda z: z / (1 + math.exp(-z)))
+    sg, su = math.sqrt(vg), math.sqrt(vu)
+    mu = second = 0.0
+    for node, mass in zip(GH_NODES, GH_WEIGHTS):
+        a = act(g + node * sg)
+        mu += mass * a * u
+        second += mass * a * a * (u * u + su * su)
+    paid = f32(torch.tensor(act(g) * u).bfloat16().item())
+    risk = norm * norm * max(second - mu * mu, 0.0)
+    risk += (norm * mu - alpha * paid) ** 2 + (beta * paid) ** 2
+    return risk * weight * weight
+
+
+def test_scores_against_float64_formulas():
+    rng = np.random.default_rng(3)
+    for _ in range(300):
+        g, u = (float(v) for v in np.float32(rng.normal(size=2) * 3))
+        vg, vu = (float(v) for v in np.float32(rng.uniform(0, 0.3, size=2)))
+        norm, weight = float(np.float32(rng.uniform(0.1, 2))), float(np.float32(rng.uniform(0, 1)))
+        alpha, beta = (float(v) for v in np.float32(rng.normal(size=2)))
+        gb = f32(torch.tensor(g).bfloat16().item())
+        ub = f32(torch.tensor(u).bfloat16().item())
+        point = oracle.score_one(g, u, vg, vu, norm, weight, alpha, beta, point=True)
+        want = (norm * (gb / (1 + math.exp(-gb))) * ub) ** 2 * weight**2
+        assert point == pytest.approx(want, rel=2e-6, abs=1e-30)
+        gh = oracle.score_one(g, u, vg, vu, norm, weight, alpha, beta, point=False)
+        assert gh == pytest.approx(gh5_reference(gb, ub, vg, vu, norm, weight, alpha, beta),
+                                   rel=1e-4, abs=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# rotation, mask and grid
+
+
+def test_rotation_and_mask_match_torch_restatement():
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(4, 512, generator=gen).bfloat16()
+    x[1] = torch.randint(-2, 3, (512,), generator=gen).bfloat16()  # integer ties
+    x[3] = 0  # all-zero row: lowest coordinates are kept
+    signs = block_hadamard_signs(512, "cpu")
+    planes, coords, qvals, qexp, norm2 = oracle.rotate(bits(x), signs.numpy(), 80)
+    rotated = mask_rotated_blocks(rotate_blocks(x.float(), signs), 80).reshape(4, 4, 128)
+    for t in range(4):
+        for b in range(4):
+            kept = np.flatnonzero(
+                torch.isin(torch.arange(128), torch.tensor(coords[t, b])).numpy())
+            assert np.array_equal(coords[t, b], kept)  # ascending coordinates
+            assert np.array_equal(planes[t, b], rotated[t, b, kept].numpy())
+            magnitude = rotated[t, b].abs()
+            order = sorted(range(128), key=lambda c: (-float(magnitude[c]), c))[:80]
+            full = rotate_blocks(x.float(), signs).reshape(4, 4, 128)[t, b].abs()
+            order = sorted(range(128), key=lambda c: (-float(full[c]), c))[:80]
+            assert sorted(order) == coords[t, b].tolist()
+    assert np.array_equal(coords[3, 0], np.arange(80))
+    # squared norms of the kept values (the tree order is the kernel's)
+    torch.testing.assert_close(
+        torch.from_numpy(norm2).double(),
+        torch.from_numpy(planes).double().square().sum(-1), rtol=1e-6, atol=0)
+
+
+def test_grid_quantisation_bounds():
+    gen = torch.Generator().manual_seed(12)
+    x = (torch.randn(8, 1024, generator=gen) * torch.logspace(-20, 20, 8)[:, None]).bfloat16()
+    signs = block_hadamard_signs(1024, "cpu")
+    planes, _, qvals, qexp, _ = oracle.rotate(bits(x), signs.numpy(), 80)
+    assert np.abs(qvals).max() <= 2**20
+    for t in range(8):
+        for b in range(8):
+            peak = np.abs(qvals[t, b]).max()
+            assert 2**19 <= peak <= 2**20
+            grid = np.ldexp(1.0, -int(qexp[t, b]))
+            err = np.abs(qvals[t, b] * grid - planes[t, b].astype(np.float64))
+            assert err.max() <= grid / 2
+
+
+# ---------------------------------------------------------------------------
+# screen
+
+
+def small_layer(tokens=3, seed=5, width=256, hidden=512, experts=8, top_k=4, rank=16):
+    return make_layer(hidden=hidden, width=width, experts=experts, top_k=top_k, rank=rank,
+                      tokens=tokens, seed=seed)
+
+
+def test_screen_is_the_exact_grid_sum_then_fixed_fma_chain():
+    layer = small_layer(tokens=2)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    w = cpu_weights(layer)
+    r = oracle.forward(w, bits(layer.hidden), layer.ids.numpy(), layer.weights.numpy(),
+                       final_count=plan.final_count, keep=80)
+    trits = unpack_sketch(layer.codes, 512, 512).numpy().astype(np.int64)  # [E, 2I, H]
+    scale = layer.statistics[..., 0].float().numpy()  # [E, 2I, B]
+    blocks, splits, span = 4, 4, 1
+    rng = np.random.default_rng(0)
+    for t in range(2):
+        for k in range(4):
+            e = int(r["ids"][t, k])
+            for row in rng.choice(512, 24, replace=False):
+                estimate = 0.0
+                for s in range(splits):
+                    part = 0.0
+                    for b in range(s * span, (s + 1) * span):
+                        coords = r["coordinates"][t, b]
+                        exact = int((trits[e, row, b * 128 + coords] * r["qvals"][t, b]).sum())
+                        dot = float(np.ldexp(np.float32(exact), -int(r["qexp"][t, b])))
+                        part = exact_fmaf(dot, float(scale[e, row, b]), part)
+                    estimate = part if s == 0 else f32(estimate + part)
+                got = r["partial"][t, row // 256, k * 256 + row % 256]
+                if r["selected"][t, k * 256 + row % 256]:
+                    continue  # exact rows are overwritten later in the call
+                assert got == np.float32(estimate), (t, k, row)
+
+
+def float64_reference(layer, plan, point=True, gelu=False, padding=None):
+    """Independent float64 restatement of the reader (reference test recipe)."""
+    h, i, k = plan.hidden_size, plan.expert_width, plan.top_k
+    n, f = plan.candidate_count, plan.final_count
+    signs = block_hadamard_signs(h, "cpu")
+    trits = unpack_sketch(layer.codes, 2 * i, h).double()
+    scale = layer.statistics[..., 0].double().repeat_interleave(128, -1)
+    resid = layer.statistics[..., 1].double()
+    sketch = trits * scale
+    act = (lambda z: torch.nn.functional.gelu(z, approximate="tanh")) if gelu \
+        else torch.nn.functional.silu
+    gu = layer.gate_up.double()
+    down = layer.down.double()
+    enc = layer.encoder.double()
+    dec = layer.decoder.double()
+    norms = layer.down.float().square().sum(1).sqrt().double()
+    outs, chosen, projections, scores_all = [], [], [], []
+    for t in range(layer.hidden.shape[0]):
+        active = padding is None or not bool(padding[t])
+        x = layer.hidden[t].float() if active else torch.zeros(h)
+        xr = mask_rotated_blocks(rotate_blocks(x[None], signs), plan.screen_coordinates)[0]
+        order = torch.argsort(layer.ids[t], stable=True)
+        experts = layer.ids[t, order].long()
+        route = layer.weights[t, order].double() if active else torch.zeros(k, dtype=torch.float64)
+        proj = torch.stack([sketch[e] @ xr.double() for e in experts])  # [K, 2I]
+        g = proj[:, :i].reshape(-1)
+        u = proj[:, i:].reshape(-1)
+        gb = g.float().bfloat16().double()
+        ub = u.float().bfloat16().double()
+        nrm = torch.cat([norms[e] for e in experts])
+        wt = route.repeat_interleave(i)
+        if point:
+            score = (nrm * act(gb) * ub).square() * wt.square()
+        else:
+            energy = xr.double().reshape(-1, 128).square().sum(-1)
+            var = torch.stack([resid[e] @ energy for e in experts])
+            sg, su = var[:, :i].reshape(-1).sqrt(), var[:, i:].reshape(-1).sqrt()
+            mu = torch.zeros_like(gb)
+            second = torch.zeros_like(gb)
+            for node, mass in zip(GH_NODES, GH_WEIGHTS):
+                a = act(gb + node * sg)
+                mu += mass * a * ub
+                second += mass * a.square() * (ub.square() + su.square())
+            # recovery geometry: alpha along each down column, beta across it
+            alpha, beta = [], []
+            for e in experts:
+                response = (dec @ enc[e]).T  # [I, H]: U B_e per channel
+                a_e = (down[e].T * response).sum(-1) / norms[e].clamp_min(1e-30)
+                alpha.append(a_e)
+                beta.append((response.square().sum(-1) - a_e.square()).clamp_min(0).sqrt())
+            alpha, beta = torch.cat(alpha), torch.cat(beta)
+            paid = (act(gb) * ub).float().bfloat16().double()
+            score = nrm.square() * (second - mu.square()).clamp_min(0)
+            score = score + (nrm * mu - alpha * paid).square() + (beta * paid).square()
+            score = score * wt.square()
+        kept = score.argsort(descending=True, stable=True)[:f].sort().values
+        mask = torch.zeros(n, dtype=torch.bool)
+        mask[kept] = True
+        exact = []
+        for e in experts:
+            ge, ue = (gu[e] @ x.double()).chunk(2)
+            ge = ge.float().bfloat16().double()
+            ue = ue.float().bfloat16().double()
+            exact.append((act(ge).float().bfloat16().double() * ue).float().bfloat16().double())
+        exact = torch.cat(exact)
+        partial = (act(gb) * ub).float().bfloat16().double()
+        feature = torch.where(mask, exact, partial)
+        routed = torch.zeros(h, dtype=torch.float64)
+        latent = torch.zeros(enc.shape[1], dtype=torch.float64)
+        for slot, e in enumerate(experts):
+            span = slice(slot * i, (slot + 1) * i)
+            value = down[e] @ (exact[span] * mask[span])
+            routed += value.float().bfloat16().double() * route[slot]
+            z = enc[e] @ (feature[span] * ~mask[span])
+            latent += z.float().bfloat16().double() * route[slot]
+        correction = (dec @ latent.float().bfloat16().double()).float().bfloat16().double()
+        if not active:
+            correction = torch.zeros_like(correction)
+        outs.append((routed + correction).float().bfloat16())
+        chosen.append(mask)
+        projections.append(torch.stack((g, u)))
+        scores_all.append(score)
+    return (torch.stack(outs), torch.stack(chosen), torch.stack(projections),
+            torch.stack(scores_all))
+
+
+@pytest.mark.parametrize("point", [True, False])
+def test_oracle_matches_float64_reference(point):
+    layer = small_layer(tokens=4, seed=9)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    w = cpu_weights(layer, point=point)
+    padding = np.array([0, 0, 1, 0], np.uint8)
+    r = oracle.forward(w, bits(layer.hidden), layer.ids.numpy(), layer.weights.numpy(),
+                       final_count=plan.final_count, keep=80, point=point, padding=padding)
+    out, chosen, projected, scores = float64_reference(layer, plan, point=point,
+                                                       padding=torch.from_numpy(padding))
+    active = padding == 0
+    # projections of skipped channels (exact rows are overwritten)
+    skipped = ~r["selected"].astype(bool)
+    for t in np.flatnonzero(active):
+        got = torch.from_numpy(r["partial"][t]).double()
+        torch.testing.assert_close(got[:, skipped[t]], projected[t][:, skipped[t]],
+                                   rtol=2e-4, atol=2e-5)
+    torch.testing.assert_close(torch.from_numpy(r["scores"][active]).double(),
+                               scores[active], rtol=0.025, atol=1e-9)
+    # selection: identical except within the rounding band around the cutoff
+    for t in np.flatnonzero(active):
+        s = scores[t]
+        cutoff = s.sort(descending=True).values[plan.final_count - 1]
+        error = (torch.from_numpy(r["scores"][t]).double() - s).abs().max()
+        flipped = torch.from_numpy(r["selected"][t].astype(bool)) ^ chosen[t]
+        assert bool(((s - cutoff).abs() <= 2 * error)[flipped].all())
+        assert int(r["selected"][t].sum()) == plan.final_count
+    got = torch.from_numpy(oracle.bf16_to_float(r["out"])).double()
+    torch.testing.assert_close(got[active], out.double()[active], rtol=0.04, atol=0.02)
+    assert not got[~active].any()
+
+
+def test_selection_is_the_stable_top_f_of_the_scores():
+    layer = small_layer(tokens=3, seed=21)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.2,
+                          screen_keep=0.625)
+    r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80)
+    for t in range(3):
+        keys = r["scores"][t] + np.float32(0)
+        order = np.lexsort((np.arange(len(keys)), -keys.astype(np.float64)))
+        top = np.sort(order[: plan.final_count])
+        assert np.array_equal(r["next_ids"][t], top)
+        mask = np.zeros(len(keys), np.uint8)
+        mask[top] = 1
+        assert np.array_equal(r["selected"][t], mask)
+        counts = mask.reshape(4, 256).sum(1)
+        assert np.array_equal(r["counts"][t], counts)
+        assert np.array_equal(r["starts"][t], np.cumsum(counts) - counts)
+        tiles = (counts + 127) // 128
+        assert np.array_equal(r["tile_starts"][t], np.cumsum(tiles) - tiles)
+
+
+def test_all_zero_input_selects_lowest_ids_and_padding():
+    layer = small_layer(tokens=2, seed=23)
+    layer.hidden.zero_()
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80,
+                       padding=np.array([0, 1], np.uint8))
+    for t in range(2):
+        assert np.array_equal(r["next_ids"][t], np.arange(plan.final_count))
+    assert not np.any(oracle.bf16_to_float(r["out"]))
+
+
+def test_threshold_keeps_scores_at_or_above_tau_capped_at_f():
+    layer = small_layer(tokens=2, seed=29)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    base = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                          layer.weights.numpy(), final_count=plan.final_count, keep=80)
+    tau = float(np.sort(base["scores"][0])[::-1][40])
+    r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80,
+                       threshold=tau)
+    for t in range(2):
+        passing = np.flatnonzero(base["scores"][t] >= np.float32(tau))
+        if len(passing) <= plan.final_count:
+            want = passing
+        else:
+            keys = base["scores"][t]
+            order = np.lexsort((np.arange(len(keys)), -keys.astype(np.float64)))
+            want = np.sort(order[: plan.final_count])
+        got = r["next_ids"][t]
+        assert np.array_equal(got[: len(want)], want)
+        assert np.all(got[len(want):] == -1)
+
+
+def test_exact_rows_are_lane_ordered_dots():
+    rng = np.random.default_rng(4)
+    row = torch.from_numpy(rng.normal(size=2048).astype(np.float32)).bfloat16()
+    x = torch.from_numpy(rng.normal(size=2048).astype(np.float32)).bfloat16()
+    got = oracle.row_dot(bits(row), bits(x))
+    # restatement of the lane order: lane partial fma chains then a pairwise tree
+    lanes = []
+    for lane in range(64):
+        acc = 0.0
+        for j in range(4):
+            for i in range(8):
+                h = 512 * j + 8 * lane + i
+                acc = exact_fmaf(float(row[h].float()), float(x[h].float()), acc)
+        lanes.append(acc)
+    step = 1
+    while step < 64:
+        lanes = [f32(lanes[2 * i] + lanes[2 * i + 1]) for i in range(len(lanes) // 2)]
+        step *= 2
+    assert got == np.float32(lanes[0])
+    assert got == pytest.approx(float(row.double() @ x.double()), rel=1e-5, abs=1e-5)
+
+
+def test_dense_stock_on_retained_subset():
+    """The routed part equals the dense expert restricted to the kept channels."""
+    layer = small_layer(tokens=2, seed=31)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80)
+    for t in range(2):
+        order = np.argsort(layer.ids[t].numpy(), kind="stable")
+        dense = torch.zeros(512, dtype=torch.float64)
+        for slot, o in enumerate(order):
+            e = int(layer.ids[t, o])
+            gate, up = (layer.gate_up[e].double() @ layer.hidden[t].double()).chunk(2)
+            a = torch.nn.functional.silu(gate) * up
+            keep = torch.from_numpy(r["selected"][t, slot * 256:(slot + 1) * 256].astype(bool))
+            dense += float(layer.weights[t, o]) * (layer.down[e].double()[:, keep] @ a[keep])
+        routed = torch.from_numpy(
+            (r["values"][t] * r["weights"][t][:, None]).sum(0)).double()
+        torch.testing.assert_close(routed, dense, rtol=1e-2, atol=2e-3)
