@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 POINT = 1
 GELU = 2
@@ -83,6 +83,11 @@ WORKSPACE_FIELDS = (
     ("down_parts", "float32"),
     ("encoder_parts", "float32"),
     ("latent", "float32"),
+    ("group_experts", "int32"),
+    ("group_starts", "int32"),
+    ("group_counts", "int32"),
+    ("group_pairs", "int32"),
+    ("group_total", "int32"),
 )
 
 

@@ -205,6 +205,12 @@ class ReaderWorkspace:
             "encoder_parts", (capacity, k, self.encoder_splits, rank)
         )
         self.latent = buffer("latent", (capacity, rank))
+        # Expert-major grouping of the call's (token, slot) pairs.
+        self.group_experts = buffer("group_experts", (capacity * k,))
+        self.group_starts = buffer("group_starts", (capacity * k,))
+        self.group_counts = buffer("group_counts", (capacity * k,))
+        self.group_pairs = buffer("group_pairs", (capacity * k,))
+        self.group_total = buffer("group_total", (1,))
         # The reference's last-arrival counters; these kernels need none but the
         # attributes stay (all zero) for callers that inspect them.
         self.screen_counters = torch.zeros(
@@ -234,6 +240,8 @@ class ReaderWorkspace:
             self.activations, self.completed, self.selected, *self.candidate_ids,
             *self.scores, self.starts, self.counts, self.tile_starts,
             self.down_tile_starts, self.down_parts, self.encoder_parts, self.latent,
+            self.group_experts, self.group_starts, self.group_counts, self.group_pairs,
+            self.group_total,
         )
         self.bytes = sum(t.numel() * t.element_size() for t in buffers)
         self.charged = False
@@ -271,6 +279,11 @@ _WORKSPACE_ATTRS = (
     ("down_parts", "down_parts"),
     ("encoder_parts", "encoder_parts"),
     ("latent", "latent"),
+    ("group_experts", "group_experts"),
+    ("group_starts", "group_starts"),
+    ("group_counts", "group_counts"),
+    ("group_pairs", "group_pairs"),
+    ("group_total", "group_total"),
 )
 
 
@@ -380,8 +393,11 @@ class ProgressiveReader:
             )
         if rank > 64:
             raise ValueError("Recovery rank above 64 is not supported")
-        if k > 64 or plan.candidate_count > 16384:
-            raise ValueError("At most 64 routed experts and 16384 candidates per token")
+        if k > 64 or plan.candidate_count > 16384 or max_tokens * k > 8192:
+            raise ValueError(
+                "At most 64 routed experts, 16384 candidates per token and 8192 "
+                "routed pairs per call"
+            )
         self.pdl = False
         self.screen_last_block_reduction = screen_last_block_reduction
         self.recovery_last_block_reduction = recovery_last_block_reduction and rank > 0

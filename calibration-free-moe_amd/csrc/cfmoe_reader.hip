@@ -5,8 +5,8 @@
 // ctypes. The stages follow ProgressiveReader.__call__ of the reference
 // (calibration_free_moe/reader/progressive.py:3876-4472):
 //
-//   prepare_kernel   route + rotate + mask + grid quantisation  (:143-453)
-//   screen_kernel    sketch projections per rotation-block split (:478-1108)
+//   prepare_kernel   route, expert grouping, rotate + mask + grid (:143-453)
+//   group_screen_kernel  expert-major sketch projections (MFMA)   (:478-1108)
 //   score_kernel     split sums, BF16 rounding, channel scores   (:1111-1353)
 //   select_kernel    per-token top-F (radix select + compaction) (:1584-1775)
 //   exact_kernel     native gate/up rows of kept channels         (:1372-1581)
@@ -28,7 +28,7 @@
 
 #include "cfmoe_reader.h"
 
-namespace {
+namespace cfmoe {
 
 constexpr int kWave = 64;
 
@@ -132,7 +132,50 @@ __device__ __forceinline__ uint64_t lanes_below(int lane) {
 }
 
 // ---------------------------------------------------------------------------
-// prepare: route (progressive.py:349-386) and rotate/mask (:389-453)
+// block-wide reductions (thread order)
+
+__device__ int block_sum(int v, int *scratch) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  __syncthreads();
+  if (lane == 0) scratch[wave] = v;
+  __syncthreads();
+  int total = 0;
+  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) total += scratch[w];
+  return total;
+}
+
+// Exclusive prefix over threads in thread order; *total receives the sum.
+__device__ int block_exclusive(int v, int *scratch, int *total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inclusive = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int n = __shfl_up(inclusive, o);
+    if (lane >= o) inclusive += n;
+  }
+  __syncthreads();
+  if (lane == 63) scratch[wave] = inclusive;
+  __syncthreads();
+  int before = 0, sum = 0;
+  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) {
+    if (w < wave) before += scratch[w];
+    sum += scratch[w];
+  }
+  *total = sum;
+  return before + inclusive - v;
+}
+
+// ---------------------------------------------------------------------------
+// prepare: route + expert grouping (progressive.py:349-386, :2329-2373) and
+// rotate/mask (:389-453)
+//
+// 256-thread blocks. Wave w of block i rotates cell 4 i + w = (token, block);
+// the wave of a token's block 0 also adds the token's fixed read charges. The
+// last block sorts every token's K ids, then groups the (token, slot) pairs by
+// expert: touched experts in ascending id order, each with its pairs in
+// ascending pair index (deterministic lists, no atomics in the order).
 
 struct PrepareArgs {
   const uint16_t *x;
@@ -147,51 +190,139 @@ struct PrepareArgs {
   int32_t *qvals;
   int32_t *qexp;
   float *norm2;
+  int32_t *group_experts;
+  int32_t *group_starts;
+  int32_t *group_counts;
+  int32_t *group_pairs;
+  int32_t *group_total;
   double *read_work;
   double charges[18];
-  int H, K, E, keep;
+  int T, H, K, E, keep;
   uint32_t flags;
-  int route, rotate;
+  int route, rotate, cells;
 };
 
-__global__ __launch_bounds__(64) void prepare_kernel(PrepareArgs a) {
-  const int t = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
-  const bool active = is_active(a.padding, t);
-  if (a.route && b == 0) {
-    if (lane == 0) {
-      int original[64], ordered[64];
-      for (int k = 0; k < a.K; ++k) {
-        int id = (a.flags & CFMOE_IDS_INT64)
-                     ? static_cast<int>(static_cast<const int64_t *>(a.router_ids)[t * a.K + k])
-                     : static_cast<const int32_t *>(a.router_ids)[t * a.K + k];
-        // an id outside [0, E) names no local expert: it reads nothing
-        if (id < 0 || id >= a.E) id = -1;
-        original[k] = ordered[k] = id;
-      }
-      for (int i = 1; i < a.K; ++i) {
-        int v = ordered[i], j = i - 1;
-        while (j >= 0 && ordered[j] > v) {
-          ordered[j + 1] = ordered[j];
-          --j;
-        }
-        ordered[j + 1] = v;
-      }
-      for (int k = 0; k < a.K; ++k) {
-        float w = 0.0f;
-        for (int j = 0; j < a.K; ++j) {
-          if (original[j] != ordered[k] || !active) continue;
-          float rw = (a.flags & CFMOE_WEIGHTS_BF16)
-                         ? bf16f(static_cast<const uint16_t *>(a.router_weights)[t * a.K + j])
-                         : static_cast<const float *>(a.router_weights)[t * a.K + j];
-          w += rw;
-        }
-        a.ids[t * a.K + k] = ordered[k];
-        a.weights[t * a.K + k] = w;
+constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
+constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
+constexpr int kPrepareThreads = 256;
+
+__device__ void route_and_group(const PrepareArgs &a) {
+  __shared__ __align__(16) int16_t sorted[kMaxPairs];
+  __shared__ int16_t routed[kMaxPairs];
+  __shared__ int counts[kMaxExperts];
+  __shared__ int scratch[32];
+  const int tid = threadIdx.x;
+  const int T = a.T, K = a.K;
+  const int pairs = T * K;
+  // raw ids (outside [0, E) -> -1: no local expert, reads nothing)
+  for (int p = tid; p < pairs; p += kPrepareThreads) {
+    int id = (a.flags & CFMOE_IDS_INT64)
+                 ? static_cast<int>(static_cast<const int64_t *>(a.router_ids)[p])
+                 : static_cast<const int32_t *>(a.router_ids)[p];
+    routed[p] = static_cast<int16_t>((id < 0 || id >= a.E) ? -1 : id);
+  }
+  __syncthreads();
+  // slot k of a token moves to its rank among the token's ids (ties by slot);
+  // its weight is the sum of the weights of equal ids (progressive.py:369-375)
+  for (int p = tid; p < pairs; p += kPrepareThreads) {
+    const int t = p / K, k = p % K;
+    const bool active = is_active(a.padding, t);
+    const int id = routed[p];
+    int rank = 0, equal = 0;
+    for (int j = 0; j < K; ++j) {
+      const int other = routed[t * K + j];
+      rank += other < id || (other == id && j < k);
+      equal += other == id;
+    }
+    auto weight_of = [&](int q) {
+      return (a.flags & CFMOE_WEIGHTS_BF16)
+                 ? bf16f(static_cast<const uint16_t *>(a.router_weights)[q])
+                 : static_cast<const float *>(a.router_weights)[q];
+    };
+    float w = 0.0f;
+    if (active) {
+      if (equal == 1) {
+        w = 0.0f + weight_of(p);
+      } else {
+        for (int j = 0; j < K; ++j)
+          if (routed[t * K + j] == id) w += weight_of(t * K + j);
       }
     }
-    if ((a.flags & CFMOE_ACCOUNT) && active && lane < 18 && a.charges[lane] != 0.0)
-      atomicAdd(a.read_work + lane, a.charges[lane]);
+    a.ids[t * K + rank] = id;
+    a.weights[t * K + rank] = w;
+    sorted[t * K + rank] = static_cast<int16_t>(active ? id : -1);
   }
+  const int padded = (pairs + 7) / 8 * 8;
+  for (int p = pairs + tid; p < padded; p += kPrepareThreads) sorted[p] = -1;
+  __syncthreads();
+  // thread owns the contiguous experts [first, last)
+  const int span = (a.E + kPrepareThreads - 1) / kPrepareThreads;
+  const int first = min(a.E, tid * span), last = min(a.E, first + span);
+  int touched = 0, members = 0;
+  for (int e = first; e < last; ++e) {
+    int count = 0;
+    for (int p = 0; p < padded; p += 8) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        count += static_cast<int16_t>(w[i] & 0xffffu) == e;
+        count += static_cast<int16_t>(w[i] >> 16) == e;
+      }
+    }
+    counts[e] = count;
+    touched += count > 0;
+    members += count;
+  }
+  int total_touched;
+  const int z_first = block_exclusive(touched, scratch, &total_touched);
+  int total_members;
+  int start = block_exclusive(members, scratch, &total_members);
+  int z = z_first;
+  for (int e = first; e < last; ++e) {
+    const int count = counts[e];
+    if (count == 0) continue;
+    int placed = 0;
+    for (int p = 0; p < padded && placed < count; p += 8) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (static_cast<int16_t>(w[i] & 0xffffu) == e) a.group_pairs[start + placed++] = p + 2 * i;
+        if (static_cast<int16_t>(w[i] >> 16) == e) a.group_pairs[start + placed++] = p + 2 * i + 1;
+      }
+    }
+    a.group_experts[z] = e;
+    a.group_starts[z] = start;
+    a.group_counts[z] = count;
+    ++z;
+    start += count;
+  }
+  if (tid == 0) *a.group_total = total_touched;
+  // fixed read charges: one add per slot for all active tokens (integers, exact)
+  if (a.flags & CFMOE_ACCOUNT) {
+    int active = 0;
+    for (int t = tid; t < T; t += kPrepareThreads) active += is_active(a.padding, t);
+    active = block_sum(active, scratch);
+    if (tid < 18 && a.charges[tid] != 0.0 && active > 0)
+      atomicAdd(a.read_work + tid, a.charges[tid] * static_cast<double>(active));
+  }
+}
+
+__global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
+  if (static_cast<int>(blockIdx.x) * 4 >= a.cells) {
+    if (a.route) route_and_group(a);
+    return;
+  }
+  __shared__ float compact_all[4][128];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // waves past the last cell still reach the block barrier below
+  const int cell_id = min(static_cast<int>(blockIdx.x) * 4 + wave, a.cells - 1);
+  const bool owner = static_cast<int>(blockIdx.x) * 4 + wave < a.cells;
+  const int B = a.H / 128;
+  const int t = cell_id / B, b = cell_id % B;
+  float *compact = compact_all[wave];
+  const bool active = is_active(a.padding, t);
   if (!a.rotate) return;
 
   const int H = a.H, keep = a.keep;
@@ -236,11 +367,11 @@ __global__ __launch_bounds__(64) void prepare_kernel(PrepareArgs a) {
   const uint64_t k0 = __ballot(kept0), k1 = __ballot(kept1);
   const int pos0 = __popcll(k0 & lanes_below(lane));
   const int pos1 = __popcll(k0) + __popcll(k1 & lanes_below(lane));
-  __shared__ float compact[128];
   if (kept0) compact[pos0] = v0;
   if (kept1) compact[pos1] = v1;
   __syncthreads();
-  const long cell = static_cast<long>(t) * (H / 128) + b;
+  if (!owner) return;
+  const long cell = static_cast<long>(t) * B + b;
   float sq = lane < keep ? compact[lane] * compact[lane] : 0.0f;
   if (lane + 64 < keep) sq = fmaf(compact[lane + 64], compact[lane + 64], sq);
 #pragma unroll
@@ -248,7 +379,8 @@ __global__ __launch_bounds__(64) void prepare_kernel(PrepareArgs a) {
   uint32_t peak = (kept0 ? m0 : 0u);
   peak = max(peak, kept1 ? m1 : 0u);
 #pragma unroll
-  for (int m = 1; m < 64; m <<= 1) peak = max(peak, static_cast<uint32_t>(__shfl_xor(static_cast<int>(peak), m)));
+  for (int m = 1; m < 64; m <<= 1)
+    peak = max(peak, static_cast<uint32_t>(__shfl_xor(static_cast<int>(peak), m)));
   int exponent = 0;
   if (peak) frexpf(__uint_as_float(peak), &exponent);
   const int shift = peak ? 20 - exponent : 0;
@@ -269,157 +401,422 @@ __global__ __launch_bounds__(64) void prepare_kernel(PrepareArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// screen (progressive.py:478-1108)
+// screen (progressive.py:478-1108, expert-major as :2428-2606)
 //
-// Workgroup (column group g, slot k, token t * S + split s). Lane owns one
-// 4-byte code column of every kept coordinate row: two gate and two up code
-// bytes, i.e. 10 gate and 10 up channels (20 rows). Waves split the kept
-// positions into chunks of 16 (FP32 sums of <= 16 grid values of |q| <= 2^20
-// are exact) and `sb` blocks of the split run side by side. Chunk sums are
-// combined as integers; wave 0 then applies the per-block grid exponent and
-// scale and runs the split's FMA chain in block order.
+// Workgroup = (touched expert z, block split s, group of up to kMaxChunks
+// 32-byte column chunks). A chunk's 32 code bytes per coordinate carry 160
+// trit rows (byte column j holds rows 5 j .. 5 j + 4 of one gate or up
+// channel group). For every block of the split: the expert's pairs' kept
+// coordinates and grid values are staged in LDS once, their union is formed,
+// the union's code bytes are decoded to int8 trits ([row][coordinate]) chunk
+// by chunk, and contracted with the pairs' 21-bit grid values split into
+// three int8 digits by v_mfma_i32_16x16x64_i8. Integer sums are exact, so each
+// (row, pair) gets the dot any other order would give; the block's grid
+// exponent and FP16 scale then feed the split's FMA chain in block order.
 
-struct ScreenArgs {
+struct GroupScreenArgs {
   const uint8_t *codes;
   const uint16_t *stats;
   const int32_t *coords;
   const int32_t *qvals;
   const int32_t *qexp;
   const float *norm2;
-  const int32_t *ids;
-  const uint8_t *padding;
+  const int32_t *group_experts;
+  const int32_t *group_starts;
+  const int32_t *group_counts;
+  const int32_t *group_pairs;
+  const int32_t *group_total;
   float *parts;
   float *vparts;
   long storage;
-  int H, I, K, N, keep, stride, splits, span, cn, sb, gh5;
+  int H, I, K, N, keep, stride, splits, span, chunks, per_group, gh5;
 };
 
-constexpr int kRows = 20;
+constexpr int kChunkBytes = 32;
+constexpr int kChunkRows = 5 * kChunkBytes;  // 160
+constexpr int kRowTiles = kChunkRows / 16;   // 10
+constexpr int kPairTile = 16;
+constexpr int kCoordStride = 128;            // union slots per block
+// LDS row strides, padded so that the lanes of a wave spread over the banks
+constexpr int kDigitStride = 144;            // bytes per pair row of a digit plane
+constexpr int kTritStride = 80;              // bytes per trit row (64 coordinates)
+constexpr int kRawStride = 9;                // words per staged coordinate (8 + 1)
+constexpr int kTilesPerWave = (kRowTiles + 3) / 4;
+constexpr int kMaxChunks = 4;
+constexpr int kMaxSpan = 2;  // rotation blocks per split (H <= 2048)
+constexpr int kHalfCoords = 64;  // coordinates decoded per pass
 
-__global__ __launch_bounds__(1024) void screen_kernel(ScreenArgs a) {
-  __shared__ _Float16 lut[256 * 6];
-  extern __shared__ int reduce[];
-  for (int i = threadIdx.x; i < 256; i += blockDim.x) {
-    int value = i;
-    for (int d = 0; d < 5; ++d) {
-      lut[i * 6 + d] = static_cast<_Float16>(static_cast<float>(value % 3 - 1));
-      value /= 3;
-    }
-    lut[i * 6 + 5] = static_cast<_Float16>(0.0f);
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void grid_digits(int q, int &d0, int &d1, int &d2) {
+  d0 = ((q + 128) & 255) - 128;
+  const int rest = (q - d0) >> 8;
+  d1 = ((rest + 128) & 255) - 128;
+  d2 = (rest - d1) >> 8;
+}
+
+// Chunk pipeline of the screen: codes of chunk ci + kRing are in flight (in
+// registers) while chunk ci is decoded and contracted.
+constexpr int kRing = 4;
+constexpr int kWordsPerThread = kCoordStride * (kChunkBytes / 4) / 256;  // 4
+constexpr int kMaxRows = 2048;  // 2 I rows of one expert held in LDS scale planes
+
+struct ScreenShared {
+  // One arena serves both phases. Phase 1 stages the pairs' kept coordinates
+  // and packed grid digits; phase 2 holds the trit rows of one (chunk, block,
+  // coordinate half), [160 rows][64 coords], and the chunk's code bytes of
+  // every block of the split, [block][union slot][32 bytes].
+  static constexpr int kStageCoordBytes = kMaxSpan * kPairTile * 128;
+  static constexpr int kStageBytes = kStageCoordBytes + kMaxSpan * kPairTile * 128 * 4;
+  static constexpr int kTritBytes = kChunkRows * kTritStride;
+  static constexpr int kRawWords = kCoordStride * kRawStride;
+  static constexpr int kPhase2Bytes = kTritBytes + kMaxSpan * kRawWords * 4;
+  static constexpr int kArenaBytes = kStageBytes > kPhase2Bytes ? kStageBytes : kPhase2Bytes;
+  alignas(16) uint8_t arena[kArenaBytes];
+  // Digit planes of the split's blocks: [block][digit][pair][128 union slots].
+  alignas(16) int8_t digits[kMaxSpan][3 * kPairTile * kDigitStride];
+  // FP16 scale (and residual) planes of the expert's rows for each block.
+  alignas(16) uint16_t scale[kMaxSpan][kMaxRows];
+  alignas(16) uint16_t residual[kMaxSpan][kMaxRows];
+  uint32_t lut[256][2];
+  uint32_t mask[kMaxSpan][4];
+  uint8_t union_list[kMaxSpan][128];
+  int union_count[kMaxSpan];
+  int pair_token[kPairTile], pair_slot[kPairTile];
+  int pair_shift[kMaxSpan][kPairTile];
+  float pair_norm2[kMaxSpan][kPairTile];
+};
+
+// Byte d of each of four words, packed into one word (v_perm_b32).
+__device__ __forceinline__ uint32_t gather_byte(uint32_t w0, uint32_t w1, uint32_t w2,
+                                                uint32_t w3, int d) {
+  const uint32_t select = static_cast<uint32_t>(d) | (static_cast<uint32_t>(4 + d) << 8) |
+                          0x0c0c0000u;
+  const uint32_t low = __builtin_amdgcn_perm(w1, w0, select);
+  const uint32_t high = __builtin_amdgcn_perm(w3, w2, select);
+  return __builtin_amdgcn_perm(high, low, 0x05040100u);
+}
+
+struct ScreenContext {
+  const GroupScreenArgs &a;
+  ScreenShared &sh;
+  int tid, lane, wave, e, B, body, c_begin, c_count, b_begin, blocks, count, s;
+  const uint8_t *expert_codes;
+  // body-layout code byte offset (chunk 0) of each staged word; -1 when dead
+  int fetch_base[kMaxSpan][kWordsPerThread];
+  // per MFMA output row: code byte (low 8 bits) and channel within the chunk
+  int row_info[kTilesPerWave * 4];
+
+  __device__ int8_t *trits() const { return reinterpret_cast<int8_t *>(sh.arena); }
+  __device__ uint32_t *raw(int bl) const {
+    return reinterpret_cast<uint32_t *>(sh.arena + ScreenShared::kTritBytes) +
+           bl * ScreenShared::kRawWords;
   }
-  __syncthreads();
 
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int chunk = wave % a.cn, sub = wave / a.cn;
-  const int column = blockIdx.x * kWave + lane;
-  const int body = a.stride - a.stride % 32;
-  const bool column_ok = column < a.stride / 4;
-  const int k = blockIdx.y;
-  const int t = blockIdx.z / a.splits, s = blockIdx.z % a.splits;
-  const int B = a.H / 128;
-  const bool active = is_active(a.padding, t);
-  const int e = a.ids[t * a.K + k];
-  const bool local = active && e >= 0;
-  const int b_begin = s * a.span;
-  const int b_end = min(B, (s + 1) * a.span);
-  const uint8_t *expert_codes = a.codes + static_cast<long>(local ? e : 0) * a.storage;
-  const int rows2 = 2 * a.I;
-
-  float part[kRows], vpart[kRows];
+  __device__ void setup_rows() {
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) part[i] = vpart[i] = 0.0f;
-
-  for (int group = b_begin; group < b_end; group += a.sb) {
-    const int b = group + sub;
-    int isum[kRows];
+    for (int ti = 0; ti < kTilesPerWave; ++ti)
 #pragma unroll
-    for (int i = 0; i < kRows; ++i) isum[i] = 0;
-    if (local && b < b_end && column_ok) {
-      const long cell = static_cast<long>(t) * B + b;
-      const int p0 = chunk * 16;
-      const int p1 = min(a.keep, p0 + 16);
-      uint32_t words[16];
-      float q[16];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int p = p0 + j;
-        words[j] = 0x79797979u;
-        q[j] = 0.0f;
-        if (p < p1) {
-          const int coord = a.keep < 128 ? a.coords[cell * a.keep + p] : p;
-          q[j] = static_cast<float>(a.qvals[cell * a.keep + p]);
-          long offset;
-          if (4 * column < body)
-            offset = (static_cast<long>(b) * 128 + coord) * body + 4 * column;
-          else
-            offset = static_cast<long>(B) * 128 * body +
-                     (static_cast<long>(b / 2) * 128 + coord) * 32 + (b % 2) * 16 +
-                     (4 * column - body);
-          words[j] = __builtin_nontemporal_load(
-              reinterpret_cast<const uint32_t *>(expert_codes + offset));
-        }
+      for (int r = 0; r < 4; ++r) {
+        const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
+        const int j = row / 5, d = row % 5;
+        row_info[ti * 4 + r] = j | ((5 * (j / 2) + d) << 8);
       }
-      float acc[kRows];
+  }
+
+  // Offsets of the union coordinates' code words of this pair tile.
+  __device__ void setup_fetch() {
 #pragma unroll
-      for (int i = 0; i < kRows; ++i) acc[i] = 0.0f;
+    for (int bl = 0; bl < kMaxSpan; ++bl)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-#pragma unroll
-        for (int byte = 0; byte < 4; ++byte) {
-          const int code = (words[j] >> (8 * byte)) & 255;
-          const _Float16 *entry = lut + code * 6;
-#pragma unroll
-          for (int d = 0; d < 5; ++d)
-            acc[byte * 5 + d] = fmaf(static_cast<float>(entry[d]), q[j], acc[byte * 5 + d]);
-        }
+      for (int i = 0; i < kWordsPerThread; ++i) {
+        const int item = tid + 256 * i;
+        const int u = item / 8, w = item % 8;
+        const bool live = bl < blocks && u < sh.union_count[bl];
+        fetch_base[bl][i] =
+            live ? ((b_begin + bl) * 128 + sh.union_list[bl][u]) * body + 4 * w : -1;
       }
+  }
+
+  // Issue the loads of chunk ci's code words for every block (4 per thread).
+  // The last chunk of a stride that is not a multiple of 32 bytes lives in
+  // the block-paired 16-byte tail section.
+  __device__ void fetch(int ci, uint32_t (&staged)[kMaxSpan][kWordsPerThread]) const {
+    const int g0 = (c_begin + ci) * kChunkBytes;
+    const bool tail = g0 >= body;
 #pragma unroll
-      for (int i = 0; i < kRows; ++i) isum[i] = static_cast<int>(acc[i]);
+    for (int bl = 0; bl < kMaxSpan; ++bl) {
+#pragma unroll
+      for (int i = 0; i < kWordsPerThread; ++i) {
+        staged[bl][i] = 0x79797979u;
+        const int item = tid + 256 * i;
+        if (ci >= c_count || fetch_base[bl][i] < 0) continue;
+        int offset = fetch_base[bl][i] + g0;
+        if (tail) {
+          const int w = item % 8;
+          if (w >= (a.stride - g0) / 4) continue;
+          const int b = b_begin + bl;
+          offset = B * 128 * body + ((b / 2) * 128 + sh.union_list[bl][item / 8]) * 32 +
+                   (b % 2) * 16 + 4 * w;
+        }
+        staged[bl][i] =
+            __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(expert_codes + offset));
+      }
     }
-#pragma unroll
-    for (int i = 0; i < kRows; ++i) reduce[(wave * kRows + i) * kWave + lane] = isum[i];
+  }
+
+  // Decode, contract and chain chunk ci whose code words are in `staged`.
+  __device__ void process(int ci, const uint32_t (&staged)[kMaxSpan][kWordsPerThread]) const {
+    const int chunk = c_begin + ci;
+    const int g0 = chunk * kChunkBytes;
+    const int nbytes = min(kChunkBytes, a.stride - g0);
     __syncthreads();
-    if (wave == 0 && column_ok && local) {
-      for (int si = 0; si < a.sb; ++si) {
-        const int bb = group + si;
-        if (bb >= b_end) break;
-        const long cell = static_cast<long>(t) * B + bb;
-        const int shift = a.qexp[cell];
-        const float n2 = a.gh5 ? a.norm2[cell] : 0.0f;
-        const uint16_t *plane = a.stats + (static_cast<long>(e) * B + bb) * 2 * rows2;
 #pragma unroll
-        for (int i = 0; i < kRows; ++i) {
-          int total = 0;
-          for (int ch = 0; ch < a.cn; ++ch)
-            total += reduce[((si * a.cn + ch) * kRows + i) * kWave + lane];
-          const int byte = i / 5, d = i % 5;
-          const int channel = 5 * (2 * column + byte / 2) + d;
-          if (channel < a.I) {
-            const int row = (byte % 2) * a.I + channel;
-            const float dot = ldexpf(static_cast<float>(total), -shift);
-            const float scale = static_cast<float>(__builtin_bit_cast(_Float16, plane[row]));
-            part[i] = fmaf(dot, scale, part[i]);
+    for (int bl = 0; bl < kMaxSpan; ++bl)
+#pragma unroll
+      for (int i = 0; i < kWordsPerThread; ++i) {
+        const int item = tid + 256 * i;
+        raw(bl)[(item / 8) * kRawStride + item % 8] = staged[bl][i];
+      }
+    float part[kTilesPerWave * 4], vpart[kTilesPerWave * 4];
+    bool valid[kTilesPerWave * 4];
+    int expert_row[kTilesPerWave * 4];
+#pragma unroll
+    for (int i = 0; i < kTilesPerWave * 4; ++i) {
+      part[i] = vpart[i] = 0.0f;
+      const int byte = row_info[i] & 255, channel = 80 * chunk + (row_info[i] >> 8);
+      valid[i] = byte < nbytes && channel < a.I;
+      expert_row[i] = valid[i] ? (byte % 2) * a.I + channel : 0;
+    }
+    int8_t *tr = trits();
+    const int pp = lane % 16;
+    for (int bl = 0; bl < blocks; ++bl) {
+      const int U = sh.union_count[bl];
+      const uint32_t *rw = raw(bl);
+      v4i acc[kTilesPerWave][3];
+#pragma unroll
+      for (int ti = 0; ti < kTilesPerWave; ++ti)
+#pragma unroll
+        for (int d = 0; d < 3; ++d) acc[ti][d] = v4i{0, 0, 0, 0};
+      for (int half = 0; half * kHalfCoords < U; ++half) {
+        __syncthreads();
+        // decode: byte column j of 4 consecutive union positions -> 5 trit rows
+#pragma unroll
+        for (int round = 0; round < 2; ++round) {
+          const int item = tid + 256 * round;
+          // a wave covers 8 coordinate groups x 8 byte columns
+          const int u4 = (item % 8) + 8 * ((item / 64) % 2);
+          const int j = (item / 8) % 8 + 8 * (item / 128);
+          if (j >= nbytes) continue;
+          const int u0 = half * kHalfCoords + u4 * 4;
+          uint32_t lo[4], hi[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t word = rw[(u0 + i) * kRawStride + j / 4];
+            const uint32_t code = (word >> (8 * (j % 4))) & 255u;
+            lo[i] = sh.lut[code][0];
+            hi[i] = sh.lut[code][1];
+          }
+          int8_t *out = &tr[j * 5 * kTritStride + u4 * 4];
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            *reinterpret_cast<uint32_t *>(out + d * kTritStride) =
+                gather_byte(lo[0], lo[1], lo[2], lo[3], d);
+          *reinterpret_cast<uint32_t *>(out + 4 * kTritStride) =
+              gather_byte(hi[0], hi[1], hi[2], hi[3], 0);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int ti = 0; ti < kTilesPerWave; ++ti) {
+          const int tile = wave + 4 * ti;
+          if (tile >= kRowTiles) break;
+          const int k0 = 16 * (lane / 16);
+          const v4i av =
+              *reinterpret_cast<const v4i *>(&tr[(tile * 16 + lane % 16) * kTritStride + k0]);
+#pragma unroll
+          for (int d = 0; d < 3; ++d) {
+            const v4i bv = *reinterpret_cast<const v4i *>(
+                &sh.digits[bl][(d * kPairTile + pp) * kDigitStride + half * kHalfCoords + k0]);
+            acc[ti][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[ti][d], 0, 0, 0);
+          }
+        }
+      }
+      if (pp < count) {
+        const int shift = sh.pair_shift[bl][pp];
+        const float norm2 = sh.pair_norm2[bl][pp];
+#pragma unroll
+        for (int ti = 0; ti < kTilesPerWave; ++ti) {
+          if (wave + 4 * ti >= kRowTiles) break;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = ti * 4 + r;
+            const int sum = acc[ti][0][r] + (acc[ti][1][r] << 8) + (acc[ti][2][r] << 16);
+            const float dot = ldexpf(static_cast<float>(sum), -shift);
+            const float sc =
+                static_cast<float>(__builtin_bit_cast(_Float16, sh.scale[bl][expert_row[i]]));
+            part[i] = fmaf(dot, sc, part[i]);
             if (a.gh5) {
-              const float resid =
-                  static_cast<float>(__builtin_bit_cast(_Float16, plane[rows2 + row]));
-              vpart[i] = fmaf(resid, n2, vpart[i]);
+              const float rs = static_cast<float>(
+                  __builtin_bit_cast(_Float16, sh.residual[bl][expert_row[i]]));
+              vpart[i] = fmaf(rs, norm2, vpart[i]);
             }
           }
         }
       }
     }
-    __syncthreads();
-  }
-  if (wave != 0 || !column_ok) return;
+    // store this chunk's split partial projections
+    if (pp < count) {
+      const int t = sh.pair_token[pp], slot = sh.pair_slot[pp];
+      const long base = (static_cast<long>(t) * a.splits + s) * 2 * a.N + slot * a.I;
 #pragma unroll
-  for (int i = 0; i < kRows; ++i) {
-    const int byte = i / 5, d = i % 5;
-    const int channel = 5 * (2 * column + byte / 2) + d;
-    if (channel >= a.I) continue;
-    const long address =
-        ((static_cast<long>(t) * a.splits + s) * 2 + byte % 2) * a.N + k * a.I + channel;
-    a.parts[address] = part[i];
-    if (a.gh5) a.vparts[address] = vpart[i];
+      for (int ti = 0; ti < kTilesPerWave; ++ti) {
+        if (wave + 4 * ti >= kRowTiles) break;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = ti * 4 + r;
+          if (!valid[i]) continue;
+          const long address = base + (row_info[i] & 1) * a.N + 80 * chunk + (row_info[i] >> 8);
+          a.parts[address] = part[i];
+          if (a.gh5) a.vparts[address] = vpart[i];
+        }
+      }
+    }
+  }
+};
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void group_screen_kernel(GroupScreenArgs a) {
+  __shared__ ScreenShared sh;
+  // XCD-aware work order: consecutive work items run on one XCD (workgroups
+  // are dealt to the 8 XCDs round-robin), so the chunk groups of one expert
+  // block share that XCD's L2.
+  const int total = gridDim.x, p = blockIdx.x;
+  const int per = total / 8, extra = total % 8, xcd = p % 8;
+  const int work = xcd * per + min(xcd, extra) + p / 8;
+  const int groups_per_split = (a.chunks + a.per_group - 1) / a.per_group;
+  const int cg = work % groups_per_split;
+  const int s = (work / groups_per_split) % a.splits;
+  const int z = work / (groups_per_split * a.splits);
+  if (z >= *a.group_total) return;
+  const int tid = threadIdx.x;
+  const int e = a.group_experts[z];
+  const int members = a.group_counts[z];
+  const int first_pair = a.group_starts[z];
+  const int B = a.H / 128;
+  const int keep = a.keep;
+  const int rows2 = 2 * a.I;
+  const int b_begin = s * a.span, b_end = min(B, (s + 1) * a.span);
+  const int blocks = b_end - b_begin;
+  ScreenContext ctx{a, sh, tid, tid & 63, tid >> 6, e, B, a.stride - a.stride % 32,
+                    cg * a.per_group, min(a.per_group, a.chunks - cg * a.per_group),
+                    b_begin, blocks, 0, s, a.codes + static_cast<long>(e) * a.storage,
+                    {}, {}};
+  ctx.setup_rows();
+  uint8_t(*staged_coords)[kPairTile][128] =
+      reinterpret_cast<uint8_t(*)[kPairTile][128]>(sh.arena);
+  uint32_t(*staged_digits)[kPairTile][128] = reinterpret_cast<uint32_t(*)[kPairTile][128]>(
+      sh.arena + ScreenShared::kStageCoordBytes);
+
+  {
+    int value = tid;
+    uint32_t lo = 0, hi = 0;
+    for (int d = 0; d < 5; ++d) {
+      const uint32_t t8 = static_cast<uint8_t>(static_cast<int8_t>(value % 3 - 1));
+      if (d < 4) lo |= t8 << (8 * d); else hi = t8;
+      value /= 3;
+    }
+    sh.lut[tid][0] = lo;
+    sh.lut[tid][1] = hi;
+  }
+  // The expert's FP16 scale (and residual) planes for the split's blocks.
+  for (int item = tid; item < blocks * rows2 / 2; item += 256) {
+    const int bl = item / (rows2 / 2), r2 = item % (rows2 / 2);
+    const uint32_t *plane = reinterpret_cast<const uint32_t *>(
+        a.stats + (static_cast<long>(e) * B + b_begin + bl) * 2 * rows2);
+    reinterpret_cast<uint32_t *>(sh.scale[bl])[r2] = plane[r2];
+    if (a.gh5) reinterpret_cast<uint32_t *>(sh.residual[bl])[r2] = plane[rows2 / 2 + r2];
+  }
+
+  for (int pair_base = 0; pair_base < members; pair_base += kPairTile) {
+    const int count = min(kPairTile, members - pair_base);
+    ctx.count = count;
+    __syncthreads();
+    if (tid < count) {
+      const int pair = a.group_pairs[first_pair + pair_base + tid];
+      sh.pair_token[tid] = pair / a.K;
+      sh.pair_slot[tid] = pair % a.K;
+    }
+    if (tid < kMaxSpan * 4) sh.mask[tid / 4][tid % 4] = 0;
+    __syncthreads();
+    // Stage every block's kept coordinates and grid digits at once.
+    for (int item = tid; item < blocks * count * keep; item += 256) {
+      const int bl = item / (count * keep), rest = item % (count * keep);
+      const int pp = rest / keep, j = rest % keep;
+      const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
+      const int coord = keep < 128 ? a.coords[cell * keep + j] : j;
+      int d0, d1, d2;
+      grid_digits(a.qvals[cell * keep + j], d0, d1, d2);
+      staged_coords[bl][pp][j] = static_cast<uint8_t>(coord);
+      staged_digits[bl][pp][j] = (static_cast<uint32_t>(d0) & 255u) |
+                                 ((static_cast<uint32_t>(d1) & 255u) << 8) |
+                                 ((static_cast<uint32_t>(d2) & 255u) << 16);
+      atomicOr(&sh.mask[bl][coord >> 5], 1u << (coord & 31));
+    }
+    if (tid < blocks * count) {
+      const int bl = tid / count, pp = tid % count;
+      const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
+      sh.pair_shift[bl][pp] = a.qexp[cell];
+      sh.pair_norm2[bl][pp] = a.gh5 ? a.norm2[cell] : 0.0f;
+    }
+    for (int i = tid; i < blocks * 3 * kPairTile * kDigitStride / 16; i += 256)
+      reinterpret_cast<uint4 *>(&sh.digits[0][0])[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+    // Union lists, then the digit planes in union order.
+    for (int item = tid; item < blocks * 128; item += 256) {
+      const int bl = item / 128, c = item % 128;
+      const int word = c >> 5, bit = c & 31;
+      int before = 0;
+      for (int w = 0; w < word; ++w) before += __popc(sh.mask[bl][w]);
+      before += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
+      if ((sh.mask[bl][word] >> bit) & 1u) sh.union_list[bl][before] = static_cast<uint8_t>(c);
+      if (c == 127) sh.union_count[bl] = before + ((sh.mask[bl][word] >> bit) & 1u);
+    }
+    for (int item = tid; item < blocks * count * keep; item += 256) {
+      const int bl = item / (count * keep), rest = item % (count * keep);
+      const int pp = rest / keep, j = rest % keep;
+      const int coord = staged_coords[bl][pp][j];
+      const int word = coord >> 5, bit = coord & 31;
+      int u = 0;
+      for (int w = 0; w < word; ++w) u += __popc(sh.mask[bl][w]);
+      u += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
+      const uint32_t packed = staged_digits[bl][pp][j];
+      sh.digits[bl][(0 * kPairTile + pp) * kDigitStride + u] = static_cast<int8_t>(packed & 255u);
+      sh.digits[bl][(1 * kPairTile + pp) * kDigitStride + u] =
+          static_cast<int8_t>((packed >> 8) & 255u);
+      sh.digits[bl][(2 * kPairTile + pp) * kDigitStride + u] =
+          static_cast<int8_t>((packed >> 16) & 255u);
+    }
+    __syncthreads();
+
+    ctx.setup_fetch();
+    uint32_t ring0[kMaxSpan][kWordsPerThread], ring1[kMaxSpan][kWordsPerThread];
+    uint32_t ring2[kMaxSpan][kWordsPerThread], ring3[kMaxSpan][kWordsPerThread];
+    ctx.fetch(0, ring0);
+    ctx.fetch(1, ring1);
+    ctx.fetch(2, ring2);
+    ctx.fetch(3, ring3);
+    for (int ci = 0; ci < ctx.c_count; ci += kRing) {
+      ctx.process(ci, ring0);
+      ctx.fetch(ci + kRing, ring0);
+      if (ci + 1 >= ctx.c_count) break;
+      ctx.process(ci + 1, ring1);
+      ctx.fetch(ci + 1 + kRing, ring1);
+      if (ci + 2 >= ctx.c_count) break;
+      ctx.process(ci + 2, ring2);
+      ctx.fetch(ci + 2 + kRing, ring2);
+      if (ci + 3 >= ctx.c_count) break;
+      ctx.process(ci + 3, ring3);
+      ctx.fetch(ci + 3 + kRing, ring3);
+    }
   }
 }
 
@@ -450,18 +847,24 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreArgs a) {
   const int k = logical / a.I, c = logical % a.I;
   const long stride = 2l * a.N;
   const long base = static_cast<long>(t) * a.splits * stride + logical;
-  float g = a.parts[base], u = a.parts[base + a.N];
-  float vg = 0.0f, vu = 0.0f;
-  if (a.gh5) {
-    vg = a.vparts[base];
-    vu = a.vparts[base + a.N];
-  }
-  for (int s = 1; s < a.splits; ++s) {
-    g = g + a.parts[base + s * stride];
-    u = u + a.parts[base + s * stride + a.N];
+  const int e = a.ids[t * a.K + k];
+  const bool local = is_active(a.padding, t) && e >= 0;
+  // padding rows and absent experts are screened by no workgroup: zero
+  float g = 0.0f, u = 0.0f, vg = 0.0f, vu = 0.0f;
+  if (local) {
+    g = a.parts[base];
+    u = a.parts[base + a.N];
     if (a.gh5) {
-      vg = vg + a.vparts[base + s * stride];
-      vu = vu + a.vparts[base + s * stride + a.N];
+      vg = a.vparts[base];
+      vu = a.vparts[base + a.N];
+    }
+    for (int s = 1; s < a.splits; ++s) {
+      g = g + a.parts[base + s * stride];
+      u = u + a.parts[base + s * stride + a.N];
+      if (a.gh5) {
+        vg = vg + a.vparts[base + s * stride];
+        vu = vu + a.vparts[base + s * stride + a.N];
+      }
     }
   }
   const long address = static_cast<long>(t) * stride + logical;
@@ -471,8 +874,6 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreArgs a) {
     a.variances[address] = vg;
     a.variances[address + a.N] = vu;
   }
-  const int e = a.ids[t * a.K + k];
-  const bool local = is_active(a.padding, t) && e >= 0;
   const float norm = local ? a.norms[static_cast<long>(e) * a.I + c] : 0.0f;
   float alpha = 0.0f, beta = 0.0f;
   if (local && a.geometry) {
@@ -506,39 +907,6 @@ struct SelectArgs {
 
 constexpr int kSelectThreads = 1024;
 constexpr int kSelectKeys = 16;  // keys per thread: N <= 16384
-
-__device__ int block_sum(int v, int *scratch) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
-  __syncthreads();
-  if (lane == 0) scratch[wave] = v;
-  __syncthreads();
-  int total = 0;
-  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) total += scratch[w];
-  return total;
-}
-
-// Exclusive prefix over threads in thread order; *total receives the sum.
-__device__ int block_exclusive(int v, int *scratch, int *total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inclusive = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int n = __shfl_up(inclusive, o);
-    if (lane >= o) inclusive += n;
-  }
-  __syncthreads();
-  if (lane == 63) scratch[wave] = inclusive;
-  __syncthreads();
-  int before = 0, sum = 0;
-  for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) {
-    if (w < wave) before += scratch[w];
-    sum += scratch[w];
-  }
-  *total = sum;
-  return before + inclusive - v;
-}
 
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int histogram[2048];
@@ -961,6 +1329,9 @@ int validate(const cfmoe_dims *d) {
   const int n = d->top_k * d->width;
   if (d->final_count < 1 || d->final_count > n) return fail(CFMOE_EINVAL, "final_count must be in [1, N]");
   if (n > kSelectThreads * kSelectKeys) return fail(CFMOE_EINVAL, "N exceeds 16384 candidates");
+  if (d->experts < 1 || d->experts > kMaxExperts) return fail(CFMOE_EINVAL, "experts must be in [1, 4096]");
+  if (d->hidden > 128 * 8 * kMaxSpan) return fail(CFMOE_EINVAL, "hidden must be at most 2048");
+  if (2 * d->width > kMaxRows) return fail(CFMOE_EINVAL, "width must be at most 1024");
   return 0;
 }
 
@@ -1005,9 +1376,15 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.qvals = ws->qvals;
   a.qexp = ws->qexp;
   a.norm2 = ws->norm2;
+  a.group_experts = ws->group_experts;
+  a.group_starts = ws->group_starts;
+  a.group_counts = ws->group_counts;
+  a.group_pairs = ws->group_pairs;
+  a.group_total = ws->group_total;
   a.read_work = ws->read_work;
   if (charges && (d->flags & CFMOE_ACCOUNT))
     for (int i = 0; i < 18; ++i) a.charges[i] = charges[i];
+  a.T = tokens;
   a.H = s.H;
   a.K = s.K;
   a.E = d->experts;
@@ -1015,14 +1392,19 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.flags = d->flags;
   a.route = route;
   a.rotate = rotate;
-  dim3 grid(tokens, rotate ? s.B : 1);
-  hipLaunchKernelGGL(prepare_kernel, grid, dim3(64), 0, stream, a);
+  a.cells = tokens * (rotate ? s.B : 1);
+  const int cell_blocks = (a.cells + 3) / 4;
+  hipLaunchKernelGGL(prepare_kernel, dim3(cell_blocks + (route ? 1 : 0)), dim3(kPrepareThreads), 0,
+                     stream, a);
   return check_launch("prepare");
 }
 
-}  // namespace
+}  // namespace cfmoe
 
 extern "C" {
+
+using namespace cfmoe;
+
 
 int cfmoe_abi_version(void) { return CFMOE_ABI_VERSION; }
 
@@ -1034,7 +1416,7 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
   const Shape s = shape_of(dims);
   const int64_t cap = capacity;
   const int64_t n = s.N;
-  const int64_t table[23] = {
+  const int64_t table[28] = {
       cap * s.K * 4,                          // ids
       cap * s.K * 4,                          // weights
       cap * s.B * s.keep * 4,                 // planes
@@ -1058,8 +1440,13 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
       cap * s.max_tiles * s.H * 4,            // down_parts
       cap * s.K * s.encoder_tiles * s.R * 4,  // encoder_parts
       cap * s.R * 4,                          // latent
+      cap * s.K * 4,                          // group_experts
+      cap * s.K * 4,                          // group_starts
+      cap * s.K * 4,                          // group_counts
+      cap * s.K * 4,                          // group_pairs
+      4,                                      // group_total
   };
-  const int written = count < 23 ? count : 23;
+  const int written = count < 28 ? count : 28;
   for (int i = 0; i < written; ++i) sizes[i] = table[i];
   return written;
 }
@@ -1077,7 +1464,7 @@ int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,
 
 }  // extern "C"
 
-namespace {
+namespace cfmoe {
 
 static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weights *weights,
                       const cfmoe_workspace *workspace, const void *hidden,
@@ -1089,6 +1476,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     return fail(CFMOE_EINVAL, "NULL argument");
   if (tokens < 1 || tokens > workspace->capacity) return fail(CFMOE_EINVAL, "tokens out of range");
   const Shape s = shape_of(dims);
+  if (tokens * s.K > kMaxPairs) return fail(CFMOE_EINVAL, "tokens * top_k exceeds 8192 pairs");
   if (s.R > 0 && (!weights->encoder_t || !weights->decoder))
     return fail(CFMOE_EINVAL, "rank > 0 needs encoder and decoder");
   if ((dims->flags & CFMOE_THRESHOLD) && !weights->threshold)
@@ -1122,15 +1510,18 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   sel.thresholded = (flags & CFMOE_THRESHOLD) != 0;
 
   if (s.screened) {
-    ScreenArgs sc;
+    GroupScreenArgs sc;
     sc.codes = weights->codes;
     sc.stats = static_cast<const uint16_t *>(weights->statistics);
     sc.coords = workspace->coordinates;
     sc.qvals = workspace->qvals;
     sc.qexp = workspace->qexp;
     sc.norm2 = workspace->norm2;
-    sc.ids = workspace->ids;
-    sc.padding = padding;
+    sc.group_experts = workspace->group_experts;
+    sc.group_starts = workspace->group_starts;
+    sc.group_counts = workspace->group_counts;
+    sc.group_pairs = workspace->group_pairs;
+    sc.group_total = workspace->group_total;
     sc.parts = workspace->screen_parts;
     sc.vparts = workspace->screen_variance_parts;
     sc.storage = storage_bytes(2 * s.I, s.H);
@@ -1142,18 +1533,17 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     sc.stride = code_stride(2 * s.I);
     sc.splits = s.splits;
     sc.span = s.span;
-    sc.cn = (s.keep + 15) / 16;
-    int sb = 11 / sc.cn;
-    if (sb < 1) sb = 1;
-    if (sb > s.span) sb = s.span;
-    sc.sb = sb;
+    sc.chunks = (sc.stride + kChunkBytes - 1) / kChunkBytes;
+    // Several chunks per workgroup amortise the union and digit setup once
+    // experts hold several pairs; batch one spreads chunks over workgroups.
+    sc.per_group = tokens >= 8 ? sc.chunks : 1;
     sc.gh5 = gh5;
-    const int groups = (sc.stride / 4 + kWave - 1) / kWave;
-    const int threads = kWave * sc.cn * sc.sb;
-    const size_t lds = static_cast<size_t>(sc.cn * sc.sb) * kRows * kWave * sizeof(int);
+    const long groups_bound = tokens * s.K < dims->experts ? tokens * s.K : dims->experts;
+    const long items =
+        groups_bound * s.splits * ((sc.chunks + sc.per_group - 1) / sc.per_group);
     if (stages & (1u << CFMOE_STAGE_SCREEN)) {
-      hipLaunchKernelGGL(screen_kernel, dim3(groups, s.K, tokens * s.splits), dim3(threads),
-                         lds, stream, sc);
+      hipLaunchKernelGGL(group_screen_kernel, dim3(static_cast<unsigned>(items)), dim3(256), 0,
+                         stream, sc);
       if ((rc = check_launch("screen"))) return rc;
     }
 
@@ -1275,9 +1665,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   return check_launch("output");
 }
 
-}  // namespace
+}  // namespace cfmoe
 
 extern "C" {
+
+using namespace cfmoe;
+
 
 int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights,
                   const cfmoe_workspace *workspace, const void *hidden, const void *router_ids,

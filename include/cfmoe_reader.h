@@ -28,9 +28,15 @@
 extern "C" {
 #endif
 
+#if defined(__GNUC__)
+#define CFMOE_API __attribute__((visibility("default")))
+#else
+#define CFMOE_API
+#endif
+
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 1
+#define CFMOE_ABI_VERSION 2
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -60,7 +66,7 @@ typedef struct ihipStream_t *cfmoe_stream;
 typedef struct cfmoe_dims {
   int32_t hidden;      /* H, multiple of 128 */
   int32_t width;       /* I, multiple of 16 */
-  int32_t top_k;       /* K <= 64 */
+  int32_t top_k;       /* K <= 64; tokens * K <= 8192 per call */
   int32_t experts;     /* E local experts */
   int32_t rank;        /* R recovery rank, 0 = no recovery map, <= 64 */
   int32_t final_count; /* F, channels kept per token */
@@ -110,12 +116,17 @@ typedef struct cfmoe_workspace {
   float *down_parts;          /* [cap, F/16 + K, H] */
   float *encoder_parts;       /* [cap, K, ceil(I/64), R] */
   float *latent;              /* [cap, R] */
+  int32_t *group_experts;     /* [cap * K] touched experts, ascending */
+  int32_t *group_starts;      /* [cap * K] first pair of each in group_pairs */
+  int32_t *group_counts;      /* [cap * K] pairs of each touched expert */
+  int32_t *group_pairs;       /* [cap * K] token * K + slot, grouped by expert */
+  int32_t *group_total;       /* [1] number of touched experts */
   double *read_work;          /* [20] read statistics (progressive.py:3507-3515) */
 } cfmoe_workspace;
 
 /* Byte sizes of every workspace buffer, in struct order after `capacity`
- * (23 entries). Returns the number written. */
-int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
+ * (28 entries, read_work excluded). Returns the number written. */
+CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
                           int32_t count);
 
 /* One reader call: routed-expert output of `tokens` rows (progressive.py:
@@ -123,7 +134,7 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
  * weights [T, K] fp32/bf16; padding uint8 [T] or NULL; out bf16 [T, H].
  * charges: 18 doubles added to read_work[0..17] per active token when
  * CFMOE_ACCOUNT is set (progressive.py:4492-4524), else ignored. */
-int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights,
+CFMOE_API int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights,
                   const cfmoe_workspace *workspace, const void *hidden,
                   const void *router_ids, const void *router_weights,
                   const uint8_t *padding, void *out, int32_t tokens,
@@ -133,7 +144,7 @@ int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights,
  * workspace state that earlier stages left. For per-kernel timing and tests;
  * no reference counterpart (the reference launches its Triton kernels
  * individually from Python, progressive.py:3955-4471). */
-int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weights *weights,
+CFMOE_API int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weights *weights,
                        const cfmoe_workspace *workspace, const void *hidden,
                        const void *router_ids, const void *router_weights,
                        const uint8_t *padding, void *out, int32_t tokens,
@@ -142,14 +153,14 @@ int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weight
 /* Routing-independent input rotation ahead of the router
  * (progressive.py:3829-3873). A following cfmoe_forward with
  * CFMOE_INPUT_PREPARED set skips its own rotation. */
-int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,
+CFMOE_API int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,
                         const cfmoe_workspace *workspace, const void *hidden,
                         const uint8_t *padding, int32_t tokens, cfmoe_stream stream);
 
 /* Thread-local message of the last failing call. */
-const char *cfmoe_last_error(void);
+CFMOE_API const char *cfmoe_last_error(void);
 
-int cfmoe_abi_version(void);
+CFMOE_API int cfmoe_abi_version(void);
 
 #ifdef __cplusplus
 }

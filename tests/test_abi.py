@@ -15,7 +15,7 @@ HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "cf
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(cfmoe_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:CFMOE_API\s+)?(?:const\s+)?\w+\s*\*?\s*(cfmoe_\w+)\(", text, re.M)))
 
 
 def test_library_exports_every_declared_symbol():
