@@ -132,6 +132,71 @@ def algorithmic_bytes(reader: ProgressiveReader, tokens: int) -> dict[str, int]:
 
 STAGE_BYTES = {"screen": ("sketch",), "exact": ("gate_up",), "down": ("down",),
                "encode": ("encoder",)}
+STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "group_screen_kernel",
+                 "score": "score_kernel", "select": "select_kernel", "exact": "exact_kernel",
+                 "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
+SOURCE = os.path.join(ROOT, "calibration-free-moe_amd", "csrc", "cfmoe_reader.hip")
+PROFILES = os.path.join(ROOT, "profiles")
+PROBE_ELEMENTS = 1 << 27  # float32: 512 MiB read + 512 MiB written per probe launch
+
+
+def source_digest() -> str:
+    import hashlib
+
+    with open(SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
+def stream_probe(device, steps: int = 10) -> dict:
+    """A plain streaming kernel of known size (torch.neg over 512 MiB of float32).
+
+    Its measured rate is the box's practical HBM bandwidth; under rocprofv3
+    --pmc its FETCH_SIZE / WRITE_SIZE readings calibrate the counters.
+    """
+    src = torch.ones(PROBE_ELEMENTS, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    begin.record()
+    for _ in range(steps):
+        torch.neg(src, out=dst)
+    end.record()
+    torch.cuda.synchronize()
+    seconds = begin.elapsed_time(end) * 1e-3 / steps
+    moved = 2 * 4 * PROBE_ELEMENTS
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"kernel": "torch.neg float32", "bytes_per_launch": moved,
+            "gbps": round(moved / seconds / 1e9, 1)}
+
+
+def measured_traffic(kernel: str, config: str, tokens: int, layers: int) -> dict | None:
+    """HBM bytes per launch of `kernel` from the committed counter summary.
+
+    The summary (written by `bench.py --summarize`) holds FETCH_SIZE and
+    WRITE_SIZE means per dispatch from two rocprofv3 --pmc runs, scaled by the
+    same counters read on the streaming probe; it is used only when it was
+    taken from the current kernel source on the same workload.
+    """
+    path = os.path.join(PROFILES, f"{kernel}.{config}_t{tokens}.pmc.txt")
+    if not os.path.exists(path):
+        return None
+    fields = {}
+    with open(path) as f:
+        for line in f:
+            key, sep, value = line.partition(":")
+            if sep:
+                fields[key.strip()] = value.strip()
+    if fields.get("source_sha256_16") != source_digest():
+        return None
+    return {"bytes": float(fields["traffic_bytes_per_launch"]),
+            "read_bytes": float(fields["read_bytes_per_launch"]),
+            "write_bytes": float(fields["write_bytes_per_launch"]),
+            "scale_read": float(fields["scale_read"]),
+            "scale_write": float(fields["scale_write"]),
+            "summary": os.path.relpath(path, ROOT)}
 
 
 def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> tuple[float, list[float]]:
@@ -287,7 +352,94 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def _short_name(name: str) -> str:
+    return name.split("(")[0].split("<")[0].split("::")[-1].strip() or name[:60]
+
+
+def _rocprof_rows(directory: str, suffix: str) -> list[dict]:
+    import csv
+    import glob
+
+    rows = []
+    for path in sorted(glob.glob(os.path.join(directory, "**", f"*{suffix}"), recursive=True)):
+        with open(path) as f:
+            rows += list(csv.DictReader(f))
+    return rows
+
+
+def summarize_trace(directory: str, command: str) -> str:
+    """Per-kernel launch statistics of a rocprofv3 --kernel-trace --stats run."""
+    durations: dict[str, list[int]] = {}
+    for row in _rocprof_rows(directory, "kernel_trace.csv"):
+        name = _short_name(row["Kernel_Name"])
+        durations.setdefault(name, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    lines = [f"command: {command}", f"source_sha256_16: {source_digest()}", "",
+             f"{'kernel':34s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'total_ms':>10s}"]
+    for name, values in sorted(durations.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"{name:34s} {len(values):7d} {sum(values) / len(values) / 1e3:9.2f} "
+                     f"{min(values) / 1e3:9.2f} {max(values) / 1e3:9.2f} {sum(values) / 1e6:10.3f}")
+    return "\n".join(lines) + "\n"
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str, kernel: str, command: str) -> str:
+    """HBM traffic per launch of `kernel` from FETCH_SIZE and WRITE_SIZE passes.
+
+    Both counters are in KiB per dispatch; each is scaled by the ratio of the
+    streaming probe's known bytes to what the same counter read for it.
+    """
+    def means(directory: str, counter: str) -> dict[str, float]:
+        values: dict[str, list[float]] = {}
+        for row in _rocprof_rows(directory, "counter_collection.csv"):
+            if row["Counter_Name"] != counter:
+                continue
+            values.setdefault(_short_name(row["Kernel_Name"]), []).append(float(row["Counter_Value"]))
+        return {name: sum(v) / len(v) for name, v in values.items()}
+
+    fetch, write = means(fetch_dir, "FETCH_SIZE"), means(write_dir, "WRITE_SIZE")
+    probe = next(name for name in fetch if "neg" in name or "elementwise" in name)
+    known = 4.0 * PROBE_ELEMENTS
+    scale_read = known / (fetch[probe] * 1024.0)
+    scale_write = known / (write[probe] * 1024.0)
+    read = fetch[kernel] * 1024.0 * scale_read
+    written = write[kernel] * 1024.0 * scale_write
+    lines = [
+        f"command: {command}",
+        f"source_sha256_16: {source_digest()}",
+        f"kernel: {kernel}",
+        f"fetch_kib_per_launch: {fetch[kernel]:.1f}",
+        f"write_kib_per_launch: {write[kernel]:.1f}",
+        f"probe_kernel: {probe}",
+        f"probe_fetch_kib: {fetch[probe]:.1f}",
+        f"probe_write_kib: {write[probe]:.1f}",
+        f"probe_known_bytes_each_way: {known:.0f}",
+        f"scale_read: {scale_read:.4f}",
+        f"scale_write: {scale_write:.4f}",
+        f"read_bytes_per_launch: {read:.0f}",
+        f"write_bytes_per_launch: {written:.0f}",
+        f"traffic_bytes_per_launch: {read + written:.0f}",
+        "",
+        "all kernels (KiB per dispatch, unscaled):",
+    ]
+    for name in sorted(fetch):
+        lines.append(f"  {name:34s} FETCH_SIZE {fetch[name]:14.1f}  WRITE_SIZE {write.get(name, 0.0):14.1f}")
+    return "\n".join(lines) + "\n"
+
+
 def main() -> int:
+    if len(sys.argv) > 1 and sys.argv[1] == "--summarize":
+        # bench.py --summarize trace DIR OUT COMMAND
+        # bench.py --summarize pmc FETCH_DIR WRITE_DIR KERNEL OUT COMMAND
+        mode = sys.argv[2]
+        if mode == "trace":
+            text = summarize_trace(sys.argv[3], sys.argv[5])
+            out = sys.argv[4]
+        else:
+            text = summarize_pmc(sys.argv[3], sys.argv[4], sys.argv[5], sys.argv[7])
+            out = sys.argv[6]
+        with open(out, "w") as f:
+            f.write(text)
+        print(text)
+        return 0
     parser = argparse.ArgumentParser(description=__doc__)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20)
@@ -317,8 +469,11 @@ def main() -> int:
         sub.tokens = int(count) if count else 0
         torch.cuda.empty_cache()
         extras.append(run_config(name, sub, device))
+    probe = stream_probe(device)
     baseline = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     h, i, e, k, layers, tokens, retention, keep, description = CONFIGS[args.config]
+    kernel = STAGE_KERNELS[headline["dominant"]]
+    traffic = measured_traffic(kernel, args.config, headline["tokens"], headline["layers"])
     line = {
         "metric": METRIC,
         "value": round(headline["us_per_layer"], 3),
@@ -345,14 +500,18 @@ def main() -> int:
         "stage_us": {s: round(v, 3) for s, v in headline["stage_us"].items()},
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{headline['dominant']}_kernel",
+            "kernel": kernel,
+            "algorithmic_bytes_per_launch": round(headline["dominant_bytes"]),
+            "launch_us": round(headline["stage_us"][headline["dominant"]], 3),
             "achieved": round(headline["dominant_gbps"], 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(headline["dominant_gbps"] / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": None if traffic is None else round(traffic["bytes"]),
+            "traffic_detail": traffic,
             "layer_frac": round(headline["layer_roofline_frac"], 4),
         },
+        "stream_probe": probe,
         "cpu_baseline": baseline,
         "extra": [
             {key: (round(v, 3) if isinstance(v, float) else v) for key, v in x.items()

@@ -203,6 +203,7 @@ struct PrepareArgs {
 };
 
 constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
+constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
 
@@ -258,7 +259,8 @@ __device__ void route_and_group(const PrepareArgs &a) {
   // thread owns the contiguous experts [first, last)
   const int span = (a.E + kPrepareThreads - 1) / kPrepareThreads;
   const int first = min(a.E, tid * span), last = min(a.E, first + span);
-  int touched = 0, members = 0;
+  // an expert's pairs form tiles of at most kGroupPairs (one screen workgroup each)
+  int tiles = 0, members = 0;
   for (int e = first; e < last; ++e) {
     int count = 0;
     for (int p = 0; p < padded; p += 8) {
@@ -271,14 +273,13 @@ __device__ void route_and_group(const PrepareArgs &a) {
       }
     }
     counts[e] = count;
-    touched += count > 0;
+    tiles += (count + kGroupPairs - 1) / kGroupPairs;
     members += count;
   }
-  int total_touched;
-  const int z_first = block_exclusive(touched, scratch, &total_touched);
+  int total_tiles;
+  int z = block_exclusive(tiles, scratch, &total_tiles);
   int total_members;
   int start = block_exclusive(members, scratch, &total_members);
-  int z = z_first;
   for (int e = first; e < last; ++e) {
     const int count = counts[e];
     if (count == 0) continue;
@@ -292,13 +293,15 @@ __device__ void route_and_group(const PrepareArgs &a) {
         if (static_cast<int16_t>(w[i] >> 16) == e) a.group_pairs[start + placed++] = p + 2 * i + 1;
       }
     }
-    a.group_experts[z] = e;
-    a.group_starts[z] = start;
-    a.group_counts[z] = count;
-    ++z;
+    for (int first_pair = 0; first_pair < count; first_pair += kGroupPairs) {
+      a.group_experts[z] = e;
+      a.group_starts[z] = start + first_pair;
+      a.group_counts[z] = min(kGroupPairs, count - first_pair);
+      ++z;
+    }
     start += count;
   }
-  if (tid == 0) *a.group_total = total_touched;
+  if (tid == 0) *a.group_total = total_tiles;
   // fixed read charges: one add per slot for all active tokens (integers, exact)
   if (a.flags & CFMOE_ACCOUNT) {
     int active = 0;
@@ -436,6 +439,8 @@ constexpr int kChunkBytes = 32;
 constexpr int kChunkRows = 5 * kChunkBytes;  // 160
 constexpr int kRowTiles = kChunkRows / 16;   // 10
 constexpr int kPairTile = 16;
+constexpr int kResidentScreenGroups = 512;  // 256 CUs x 2 workgroups (LDS, VGPRs)
+static_assert(kPairTile == kGroupPairs, "a screen workgroup holds one grouping tile");
 constexpr int kCoordStride = 128;            // union slots per block
 // LDS row strides, padded so that the lanes of a wave spread over the banks
 constexpr int kDigitStride = 144;            // bytes per pair row of a digit plane
@@ -727,13 +732,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     sh.lut[tid][0] = lo;
     sh.lut[tid][1] = hi;
   }
-  // The expert's FP16 scale (and residual) planes for the split's blocks.
-  for (int item = tid; item < blocks * rows2 / 2; item += 256) {
-    const int bl = item / (rows2 / 2), r2 = item % (rows2 / 2);
-    const uint32_t *plane = reinterpret_cast<const uint32_t *>(
-        a.stats + (static_cast<long>(e) * B + b_begin + bl) * 2 * rows2);
-    reinterpret_cast<uint32_t *>(sh.scale[bl])[r2] = plane[r2];
-    if (a.gh5) reinterpret_cast<uint32_t *>(sh.residual[bl])[r2] = plane[rows2 / 2 + r2];
+  // The expert's FP16 scale (and residual) rows of the chunk range's gate and
+  // up channels, for the split's blocks (channel counts are even).
+  {
+    const int channel_begin = 80 * ctx.c_begin;
+    const int channel_end = min(a.I, 80 * (ctx.c_begin + ctx.c_count));
+    const int words = (channel_end - channel_begin) / 2;
+    for (int item = tid; item < blocks * 2 * words; item += 256) {
+      const int bl = item / (2 * words), rest = item % (2 * words);
+      const int r2 = ((rest / words) * a.I + channel_begin) / 2 + rest % words;
+      const uint32_t *plane = reinterpret_cast<const uint32_t *>(
+          a.stats + (static_cast<long>(e) * B + b_begin + bl) * 2 * rows2);
+      reinterpret_cast<uint32_t *>(sh.scale[bl])[r2] = plane[r2];
+      if (a.gh5) reinterpret_cast<uint32_t *>(sh.residual[bl])[r2] = plane[rows2 / 2 + r2];
+    }
   }
 
   for (int pair_base = 0; pair_base < members; pair_base += kPairTile) {
@@ -1135,9 +1147,12 @@ struct EncodeArgs {
   int I, K, N, R, tiles, gelu;
 };
 
+constexpr int kEncodeStride = 72;  // LDS row stride (bf16) of a staged encoder row
+
 __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   __shared__ float value[64];
   __shared__ int skipped[64];
+  __shared__ __align__(16) uint16_t coefficients[64 * kEncodeStride];
   const int tile = blockIdx.x, k = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
   const int c = tile * 64 + lane;
   const long logical = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + c;
@@ -1155,6 +1170,17 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
       const float u = bfr(a.partial[base + a.N]);
       v = bfr(cfm_activate(g, a.gelu != 0) * u);
     }
+    // this skipped channel's encoder row: R bf16 (64 B at rank 32)
+    if (local) {
+      const uint16_t *row = a.encoder_t + (static_cast<long>(e) * a.I + c) * a.R;
+      uint16_t *staged = &coefficients[lane * kEncodeStride];
+      if ((a.R & 7) == 0) {
+        for (int q = 0; q < a.R; q += 8)
+          *reinterpret_cast<uint4 *>(staged + q) = load_stream16(row + q);
+      } else {
+        for (int q = 0; q < a.R; ++q) staged[q] = row[q];
+      }
+    }
   }
   value[lane] = v;
   skipped[lane] = skip;
@@ -1163,9 +1189,7 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   float acc = 0.0f;
   for (int j = 0; j < 64; ++j) {
     if (!skipped[j]) continue;
-    const float coefficient =
-        local ? bf16f(a.encoder_t[(static_cast<long>(e) * a.I + tile * 64 + j) * a.R + lane])
-              : 0.0f;
+    const float coefficient = local ? bf16f(coefficients[j * kEncodeStride + lane]) : 0.0f;
     acc = fmaf(value[j], coefficient, acc);
   }
   a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * a.R + lane] = acc;
@@ -1245,42 +1269,103 @@ struct OutputArgs {
   int H, K, R, max_tiles, encoder_tiles;
 };
 
+constexpr int kMaxSlots = 64;        // top_k limit of the C-ABI
+constexpr int kMaxRank = 64;         // recovery rank limit of the C-ABI
+constexpr int kOutputColumns = 64;   // outputs per workgroup
+constexpr int kOutputStage = 32;     // down tiles staged in LDS per phase
+constexpr int kMaxEncoderTiles = 16; // ceil(I / 64) at I <= 1024
+
+// Workgroup = 64 outputs of one token. All loads of a phase are issued
+// together (staged through LDS); one wave then walks the sums in the fixed
+// order: tiles of a slot in order, slots in order.
 __global__ __launch_bounds__(256) void output_kernel(OutputArgs a) {
-  __shared__ float latent[64];
+  __shared__ float slot_latent[kMaxSlots * kMaxRank];
+  __shared__ float latent[kMaxRank];
+  __shared__ float staged[kOutputStage][kOutputColumns];
+  __shared__ int slot_first[kMaxSlots], slot_tiles[kMaxSlots];
+  __shared__ float slot_weight[kMaxSlots];
   const int t = blockIdx.y, tid = threadIdx.x;
-  if (tid < a.R) {
-    float mixed = 0.0f;
-    for (int k = 0; k < a.K; ++k) {
-      const float *parts = a.encoder_parts + (static_cast<long>(t) * a.K + k) * a.encoder_tiles * a.R;
-      float total = 0.0f;
-      for (int j = 0; j < a.encoder_tiles; ++j)
-        total = j == 0 ? parts[tid] : total + parts[j * a.R + tid];
-      mixed = fmaf(bfr(total), a.weights[t * a.K + k], mixed);
-    }
-    latent[tid] = mixed;
-    if (blockIdx.x == 0) a.latent[static_cast<long>(t) * a.R + tid] = mixed;
+  const int o0 = blockIdx.x * kOutputColumns;
+  const int K = a.K, R = a.R;
+  for (int k = tid; k < K; k += 256) {
+    slot_first[k] = a.down_tile_starts[t * K + k];
+    slot_tiles[k] = (a.counts[t * K + k] + 15) / 16;
+    slot_weight[k] = a.weights[t * K + k];
+  }
+  // each slot's encoder tiles summed in tile order, rounded to BF16
+  for (int item = tid; item < K * R; item += 256) {
+    const int k = item / R, r = item % R;
+    const float *parts = a.encoder_parts + (static_cast<long>(t) * K + k) * a.encoder_tiles * R + r;
+    float v[kMaxEncoderTiles];
+#pragma unroll
+    for (int j = 0; j < kMaxEncoderTiles; ++j) v[j] = j < a.encoder_tiles ? parts[j * R] : 0.0f;
+    float total = v[0];
+#pragma unroll
+    for (int j = 1; j < kMaxEncoderTiles; ++j)
+      if (j < a.encoder_tiles) total = total + v[j];
+    slot_latent[k * R + r] = bfr(total);
   }
   __syncthreads();
-  const int o = blockIdx.x * 256 + tid;
-  if (o >= a.H) return;
-  const bool active = is_active(a.padding, t);
-  float routed = 0.0f;
-  for (int k = 0; k < a.K; ++k) {
-    const int tiles = (a.counts[t * a.K + k] + 15) / 16;
-    const int first = a.down_tile_starts[t * a.K + k];
-    float total = 0.0f;
-    for (int j = 0; j < tiles && first + j < a.max_tiles; ++j) {
-      const float p = a.down_parts[(static_cast<long>(t) * a.max_tiles + first + j) * a.H + o];
-      total = j == 0 ? p : total + p;
-    }
-    routed = fmaf(bfr(total), a.weights[t * a.K + k], routed);
+  if (tid < R) {
+    float mixed = 0.0f;
+    for (int k = 0; k < K; ++k) mixed = fmaf(slot_latent[k * R + tid], slot_weight[k], mixed);
+    latent[tid] = mixed;
+    if (blockIdx.x == 0) a.latent[static_cast<long>(t) * R + tid] = mixed;
   }
+  int needed = 0;
+  for (int k = 0; k < K; ++k) needed = max(needed, slot_first[k] + slot_tiles[k]);
+  needed = min(needed, a.max_tiles);
+  const int o = o0 + tid;
+  int k = 0, j = 0;
+  float total = 0.0f, routed = 0.0f;
+  const float *parts = a.down_parts + static_cast<long>(t) * a.max_tiles * a.H + o0;
+  for (int base = 0; base < needed; base += kOutputStage) {
+    __syncthreads();
+    for (int item = tid; item < kOutputStage * kOutputColumns; item += 256) {
+      const int g = base + item / kOutputColumns, col = item % kOutputColumns;
+      staged[item / kOutputColumns][col] =
+          (g < needed && o0 + col < a.H) ? parts[static_cast<long>(g) * a.H + col] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < kOutputColumns) {
+      while (k < K) {
+        const int g = slot_first[k] + j;
+        if (j >= slot_tiles[k] || g >= a.max_tiles) {
+          routed = fmaf(bfr(total), slot_weight[k], routed);
+          ++k;
+          j = 0;
+          total = 0.0f;
+          continue;
+        }
+        if (g >= base + kOutputStage) break;
+        const float p = staged[g - base][tid];
+        total = j == 0 ? p : total + p;
+        ++j;
+      }
+    }
+  }
+  if (tid >= kOutputColumns || o >= a.H) return;
+  for (; k < K; ++k, j = 0, total = 0.0f) routed = fmaf(bfr(total), slot_weight[k], routed);
   float correction = 0.0f;
-  if (a.R > 0 && a.decoder) {
+  if (R > 0 && a.decoder) {
+    const bool active = is_active(a.padding, t);
+    const uint16_t *row = a.decoder + static_cast<long>(o) * R;
     float acc = 0.0f;
-    for (int r = 0; r < a.R; ++r) {
-      const float u = active ? bf16f(a.decoder[static_cast<long>(o) * a.R + r]) : 0.0f;
-      acc = fmaf(u, bfr(latent[r]), acc);
+    if ((R & 7) == 0) {
+      for (int q = 0; q < R; q += 8) {
+        const uint4 w = active ? *reinterpret_cast<const uint4 *>(row + q) : make_uint4(0, 0, 0, 0);
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = fmaf(__uint_as_float(wv[i] << 16), bfr(latent[q + 2 * i]), acc);
+          acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), bfr(latent[q + 2 * i + 1]), acc);
+        }
+      }
+    } else {
+      for (int r = 0; r < R; ++r) {
+        const float u = active ? bf16f(row[r]) : 0.0f;
+        acc = fmaf(u, bfr(latent[r]), acc);
+      }
     }
     correction = bfr(acc);
   }
@@ -1323,8 +1408,8 @@ int validate(const cfmoe_dims *d) {
   if (!d) return fail(CFMOE_EINVAL, "dims is NULL");
   if (d->hidden <= 0 || d->hidden % 128) return fail(CFMOE_EINVAL, "hidden must be a positive multiple of 128");
   if (d->width <= 0 || d->width % 16) return fail(CFMOE_EINVAL, "width must be a positive multiple of 16");
-  if (d->top_k < 1 || d->top_k > 64) return fail(CFMOE_EINVAL, "top_k must be in [1, 64]");
-  if (d->rank < 0 || d->rank > 64) return fail(CFMOE_EINVAL, "rank must be in [0, 64]");
+  if (d->top_k < 1 || d->top_k > kMaxSlots) return fail(CFMOE_EINVAL, "top_k must be in [1, 64]");
+  if (d->rank < 0 || d->rank > kMaxRank) return fail(CFMOE_EINVAL, "rank must be in [0, 64]");
   if (d->keep < 1 || d->keep > 128) return fail(CFMOE_EINVAL, "keep must be in [1, 128]");
   const int n = d->top_k * d->width;
   if (d->final_count < 1 || d->final_count > n) return fail(CFMOE_EINVAL, "final_count must be in [1, N]");
@@ -1534,11 +1619,23 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     sc.splits = s.splits;
     sc.span = s.span;
     sc.chunks = (sc.stride + kChunkBytes - 1) / kChunkBytes;
-    // Several chunks per workgroup amortise the union and digit setup once
-    // experts hold several pairs; batch one spreads chunks over workgroups.
-    sc.per_group = tokens >= 8 ? sc.chunks : 1;
     sc.gh5 = gh5;
-    const long groups_bound = tokens * s.K < dims->experts ? tokens * s.K : dims->experts;
+    // tiles of at most kGroupPairs pairs per touched expert
+    const long pairs = static_cast<long>(tokens) * s.K;
+    const long touched = pairs < dims->experts ? pairs : dims->experts;
+    const long groups_bound =
+        pairs < touched + pairs / kGroupPairs ? pairs : touched + pairs / kGroupPairs;
+    // Several chunks per workgroup amortise the union and digit setup once
+    // experts hold several pairs; small batches spread chunks over as many
+    // workgroups as stay resident at once (two per CU).
+    sc.per_group = sc.chunks;
+    if (tokens < 8) {
+      sc.per_group = 1;
+      while (sc.per_group < sc.chunks &&
+             groups_bound * s.splits * ((sc.chunks + sc.per_group - 1) / sc.per_group) >
+                 kResidentScreenGroups)
+        ++sc.per_group;
+    }
     const long items =
         groups_bound * s.splits * ((sc.chunks + sc.per_group - 1) / sc.per_group);
     if (stages & (1u << CFMOE_STAGE_SCREEN)) {
@@ -1661,7 +1758,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.R = s.R;
   op.max_tiles = s.max_tiles;
   op.encoder_tiles = s.encoder_tiles;
-  hipLaunchKernelGGL(output_kernel, dim3((s.H + 255) / 256, tokens), dim3(256), 0, stream, op);
+  hipLaunchKernelGGL(output_kernel, dim3((s.H + kOutputColumns - 1) / kOutputColumns, tokens),
+                     dim3(256), 0, stream, op);
   return check_launch("output");
 }
 

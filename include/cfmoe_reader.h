@@ -116,11 +116,11 @@ typedef struct cfmoe_workspace {
   float *down_parts;          /* [cap, F/16 + K, H] */
   float *encoder_parts;       /* [cap, K, ceil(I/64), R] */
   float *latent;              /* [cap, R] */
-  int32_t *group_experts;     /* [cap * K] touched experts, ascending */
-  int32_t *group_starts;      /* [cap * K] first pair of each in group_pairs */
-  int32_t *group_counts;      /* [cap * K] pairs of each touched expert */
+  int32_t *group_experts;     /* [cap * K] expert of each tile of <= 16 pairs, ascending */
+  int32_t *group_starts;      /* [cap * K] first pair of each tile in group_pairs */
+  int32_t *group_counts;      /* [cap * K] pairs of each tile (1..16) */
   int32_t *group_pairs;       /* [cap * K] token * K + slot, grouped by expert */
-  int32_t *group_total;       /* [1] number of touched experts */
+  int32_t *group_total;       /* [1] number of tiles */
   double *read_work;          /* [20] read statistics (progressive.py:3507-3515) */
 } cfmoe_workspace;
 

@@ -160,6 +160,41 @@ def test_equal_experts_tie_by_expert_id():
     assert torch.equal(scores, scores[:, :1].expand_as(scores))
 
 
+def test_hot_expert_splits_into_screen_tiles():
+    """An expert routed by more than 16 tokens is screened as several tiles of
+    at most 16 pairs (one screen workgroup each); results stay bit-exact."""
+    tokens, experts, top_k = 40, 8, 4
+    layer = make_layer(hidden=512, width=256, experts=experts, top_k=top_k, rank=16,
+                       tokens=tokens, seed=61, zipf=1.2)
+    layer.ids[:, 0] = 5  # expert 5 in every token: 40 pairs -> tiles of 16, 16, 8
+    for t in range(tokens):
+        others = [e for e in torch.randperm(experts, generator=torch.Generator().manual_seed(t)).tolist()
+                  if e != 5][: top_k - 1]
+        layer.ids[t, 1:] = torch.tensor(others)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=top_k, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+    ws = reader.workspace
+    total = int(ws.group_total.item())
+    tile_experts = ws.group_experts[:total].cpu().tolist()
+    starts = ws.group_starts[:total].cpu().tolist()
+    counts = ws.group_counts[:total].cpu().tolist()
+    pairs = ws.group_pairs[: tokens * top_k].cpu().tolist()
+    assert all(1 <= c <= 16 for c in counts)
+    assert tile_experts == sorted(tile_experts)
+    assert tile_experts.count(5) == 3 and [c for e, c in zip(tile_experts, counts) if e == 5] == [16, 16, 8]
+    sorted_ids = expected["ids"]
+    seen = []
+    for e, first, count in zip(tile_experts, starts, counts):
+        members = pairs[first:first + count]
+        assert members == sorted(members)
+        assert all(sorted_ids[p // top_k, p % top_k] == e for p in members)
+        seen += members
+    assert sorted(seen) == list(range(tokens * top_k))
+
+
 def test_threshold_selection():
     tokens = 3
     layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=48)
