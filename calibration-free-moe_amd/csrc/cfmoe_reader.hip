@@ -444,12 +444,12 @@ static_assert(kPairTile == kGroupPairs, "a screen workgroup holds one grouping t
 constexpr int kCoordStride = 128;            // union slots per block
 // LDS row strides, padded so that the lanes of a wave spread over the banks
 constexpr int kDigitStride = 144;            // bytes per pair row of a digit plane
-constexpr int kTritStride = 80;              // bytes per trit row (64 coordinates)
+constexpr int kTritStride = 144;             // bytes per trit row (128 union columns)
 constexpr int kRawStride = 9;                // words per staged coordinate (8 + 1)
 constexpr int kTilesPerWave = (kRowTiles + 3) / 4;
 constexpr int kMaxChunks = 4;
 constexpr int kMaxSpan = 2;  // rotation blocks per split (H <= 2048)
-constexpr int kHalfCoords = 64;  // coordinates decoded per pass
+constexpr int kHalfCoords = 64;  // union columns per MFMA pass (K = 64)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -462,35 +462,45 @@ __device__ __forceinline__ void grid_digits(int q, int &d0, int &d1, int &d2) {
 
 // Chunk pipeline of the screen: codes of chunk ci + kRing are in flight (in
 // registers) while chunk ci is decoded and contracted.
-constexpr int kRing = 4;
+constexpr int kRing = 2;
 constexpr int kWordsPerThread = kCoordStride * (kChunkBytes / 4) / 256;  // 4
-constexpr int kMaxRows = 2048;  // 2 I rows of one expert held in LDS scale planes
+constexpr int kMaxRows = 2048;  // 2 I rows of one expert (I <= 1024)
 
 struct ScreenShared {
   // One arena serves both phases. Phase 1 stages the pairs' kept coordinates
-  // and packed grid digits; phase 2 holds the trit rows of one (chunk, block,
-  // coordinate half), [160 rows][64 coords], and the chunk's code bytes of
-  // every block of the split, [block][union slot][32 bytes].
+  // and packed grid digits; phase 2 holds the trit tiles of one chunk for
+  // every block of the split: [block][160 rows][128 union columns].
   static constexpr int kStageCoordBytes = kMaxSpan * kPairTile * 128;
   static constexpr int kStageBytes = kStageCoordBytes + kMaxSpan * kPairTile * 128 * 4;
   static constexpr int kTritBytes = kChunkRows * kTritStride;
-  static constexpr int kRawWords = kCoordStride * kRawStride;
-  static constexpr int kPhase2Bytes = kTritBytes + kMaxSpan * kRawWords * 4;
+  static constexpr int kPhase2Bytes = kMaxSpan * kTritBytes;
   static constexpr int kArenaBytes = kStageBytes > kPhase2Bytes ? kStageBytes : kPhase2Bytes;
   alignas(16) uint8_t arena[kArenaBytes];
-  // Digit planes of the split's blocks: [block][digit][pair][128 union slots].
+  // The chunk's code words of every block: [block][union slot][8 words + 1].
+  alignas(16) uint32_t raw[kMaxSpan][kCoordStride * kRawStride];
+  // Digit planes of the split's blocks: [block][digit][pair][union column].
   alignas(16) int8_t digits[kMaxSpan][3 * kPairTile * kDigitStride];
-  // FP16 scale (and residual) planes of the expert's rows for each block.
-  alignas(16) uint16_t scale[kMaxSpan][kMaxRows];
-  alignas(16) uint16_t residual[kMaxSpan][kMaxRows];
-  uint32_t lut[256][2];
+  // FP16 scale and residual of the chunk's 160 rows for each block.
+  uint16_t scale[kMaxSpan][kChunkRows];
+  uint16_t residual[kMaxSpan][kChunkRows];
+  // code byte -> its 5 trits as int8: (t0..t3) in x, t4 in y
+  uint2 lut[256];
   uint32_t mask[kMaxSpan][4];
   uint8_t union_list[kMaxSpan][128];
   int union_count[kMaxSpan];
+  int union_groups[kMaxSpan];
   int pair_token[kPairTile], pair_slot[kPairTile];
   int pair_shift[kMaxSpan][kPairTile];
   float pair_norm2[kMaxSpan][kPairTile];
 };
+
+// Union slot u of a block with G = ceil(U / 4) slot groups sits in MFMA
+// column 4 (u % G) + u / G: the four slots of a column group are G apart, so
+// the lanes decoding consecutive groups read raw rows 9 words apart (no bank
+// conflicts), and the columns in use stay within ceil(U / 4) * 4.
+__device__ __forceinline__ int union_column(int u, int groups) {
+  return 4 * (u % groups) + u / groups;
+}
 
 // Byte d of each of four words, packed into one word (v_perm_b32).
 __device__ __forceinline__ uint32_t gather_byte(uint32_t w0, uint32_t w1, uint32_t w2,
@@ -502,31 +512,37 @@ __device__ __forceinline__ uint32_t gather_byte(uint32_t w0, uint32_t w1, uint32
   return __builtin_amdgcn_perm(high, low, 0x05040100u);
 }
 
+// Loads through the global address space (global_load, counted by vmcnt
+// only; a generic pointer would make them flat loads that LDS waits also
+// have to drain).
+template <typename T>
+__device__ __forceinline__ T load_global(const T *p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) T *>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
+// Load sources of dead lanes (no branch around a load, no select after it).
+__device__ const uint32_t kZeroCodeWord = 0x79797979u;  // four zero-trit bytes
+__device__ const uint16_t kZeroHalves[2] = {0, 0};
+
+// One chunk's loads in flight: code words of every block and the chunk's
+// FP16 scale | residual << 16 rows (2 per thread).
+struct Staged {
+  uint32_t words[kMaxSpan][kWordsPerThread];
+  uint32_t rows[2];
+};
+
+template <bool kGh5>
 struct ScreenContext {
   const GroupScreenArgs &a;
   ScreenShared &sh;
   int tid, lane, wave, e, B, body, c_begin, c_count, b_begin, blocks, count, s;
   const uint8_t *expert_codes;
-  // body-layout code byte offset (chunk 0) of each staged word; -1 when dead
-  int fetch_base[kMaxSpan][kWordsPerThread];
-  // per MFMA output row: code byte (low 8 bits) and channel within the chunk
-  int row_info[kTilesPerWave * 4];
-
-  __device__ int8_t *trits() const { return reinterpret_cast<int8_t *>(sh.arena); }
-  __device__ uint32_t *raw(int bl) const {
-    return reinterpret_cast<uint32_t *>(sh.arena + ScreenShared::kTritBytes) +
-           bl * ScreenShared::kRawWords;
-  }
-
-  __device__ void setup_rows() {
-#pragma unroll
-    for (int ti = 0; ti < kTilesPerWave; ++ti)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
-        const int j = row / 5, d = row % 5;
-        row_info[ti * 4 + r] = j | ((5 * (j / 2) + d) << 8);
-      }
+  // per staged word: body-layout code byte offset at chunk 0 (bits 0..23) and
+  // the union coordinate (bits 24..30); -1 when the word is dead
+  int fetch_info[kMaxSpan][kWordsPerThread];
+  __device__ int8_t *trits(int bl) const {
+    return reinterpret_cast<int8_t *>(sh.arena) + bl * ScreenShared::kTritBytes;
   }
 
   // Offsets of the union coordinates' code words of this pair tile.
@@ -538,112 +554,143 @@ struct ScreenContext {
         const int item = tid + 256 * i;
         const int u = item / 8, w = item % 8;
         const bool live = bl < blocks && u < sh.union_count[bl];
-        fetch_base[bl][i] =
-            live ? ((b_begin + bl) * 128 + sh.union_list[bl][u]) * body + 4 * w : -1;
+        const int coord = live ? sh.union_list[bl][u] : 0;
+        fetch_info[bl][i] =
+            live ? (((b_begin + bl) * 128 + coord) * body + 4 * w) | (coord << 24) : -1;
       }
   }
 
-  // Issue the loads of chunk ci's code words for every block (4 per thread).
-  // The last chunk of a stride that is not a multiple of 32 bytes lives in
-  // the block-paired 16-byte tail section.
-  __device__ void fetch(int ci, uint32_t (&staged)[kMaxSpan][kWordsPerThread]) const {
-    const int g0 = (c_begin + ci) * kChunkBytes;
+  // Issue the loads of chunk ci: 4 code words per block and the chunk's FP16
+  // scale (and residual) rows. The last chunk of a stride that is not a
+  // multiple of 32 bytes lives in the block-paired 16-byte tail section.
+  // Every load is issued unconditionally (dead ones read the expert's first
+  // word and are replaced), so no branch separates the loads from their uses
+  // and the wait before a chunk covers only that chunk's loads. Plain
+  // (L2-allocating) loads: the next chunks of a coordinate share its line.
+  __device__ void fetch(int ci, Staged &staged) const {
+    const int chunk = c_begin + ci;
+    const int g0 = chunk * kChunkBytes;
     const bool tail = g0 >= body;
+    const bool chunk_live = ci < c_count;
+    const int tail_words = (a.stride - g0) / 4;
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
+      const int b = b_begin + bl;
+      const int tail_base = B * 128 * body + (b / 2) * 128 * 32 + (b % 2) * 16;
 #pragma unroll
       for (int i = 0; i < kWordsPerThread; ++i) {
-        staged[bl][i] = 0x79797979u;
-        const int item = tid + 256 * i;
-        if (ci >= c_count || fetch_base[bl][i] < 0) continue;
-        int offset = fetch_base[bl][i] + g0;
-        if (tail) {
-          const int w = item % 8;
-          if (w >= (a.stride - g0) / 4) continue;
-          const int b = b_begin + bl;
-          offset = B * 128 * body + ((b / 2) * 128 + sh.union_list[bl][item / 8]) * 32 +
-                   (b % 2) * 16 + 4 * w;
-        }
-        staged[bl][i] =
-            __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(expert_codes + offset));
+        const int info = fetch_info[bl][i];
+        const int w = (tid + 256 * i) % 8;
+        const int body_offset = (info & 0xffffff) + g0;
+        const int tail_offset = tail_base + ((info >> 24) & 127) * 32 + 4 * w;
+        const bool live = chunk_live && info >= 0 && (!tail || w < tail_words);
+        const uint32_t *source =
+            live ? reinterpret_cast<const uint32_t *>(expert_codes + (tail ? tail_offset : body_offset))
+                 : &kZeroCodeWord;
+        staged.words[bl][i] = load_global(source);
       }
+    }
+    const int nbytes = min(kChunkBytes, a.stride - g0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int item = tid + 256 * k;
+      const int bl = item / kChunkRows, row = item % kChunkRows;
+      const int j = row / 5, channel = 80 * chunk + 5 * (j / 2) + row % 5;
+      const bool live = chunk_live && bl < blocks && j < nbytes && channel < a.I;
+      const uint16_t *row_source =
+          live ? a.stats + (static_cast<long>(e) * B + b_begin + bl) * 4 * a.I + (j % 2) * a.I +
+                     channel
+               : kZeroHalves;
+      uint32_t value = load_global(row_source);
+      if (kGh5) value |= static_cast<uint32_t>(load_global(row_source + (live ? 2 * a.I : 1))) << 16;
+      staged.rows[k] = value;
     }
   }
 
   // Decode, contract and chain chunk ci whose code words are in `staged`.
-  __device__ void process(int ci, const uint32_t (&staged)[kMaxSpan][kWordsPerThread]) const {
+  // Three barriers per chunk: (A) the previous chunk's trit tiles and chunk
+  // rows are consumed; (B) this chunk's code words and rows are in LDS;
+  // (C) its trit tiles are complete.
+  __device__ void process(int ci, const Staged &staged) const {
     const int chunk = c_begin + ci;
     const int g0 = chunk * kChunkBytes;
     const int nbytes = min(kChunkBytes, a.stride - g0);
-    __syncthreads();
+    __syncthreads();  // (A)
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl)
 #pragma unroll
       for (int i = 0; i < kWordsPerThread; ++i) {
         const int item = tid + 256 * i;
-        raw(bl)[(item / 8) * kRawStride + item % 8] = staged[bl][i];
+        sh.raw[bl][(item / 8) * kRawStride + item % 8] = staged.words[bl][i];
       }
-    float part[kTilesPerWave * 4], vpart[kTilesPerWave * 4];
-    bool valid[kTilesPerWave * 4];
-    int expert_row[kTilesPerWave * 4];
+    // the chunk's FP16 scale (and residual) rows of every block
 #pragma unroll
-    for (int i = 0; i < kTilesPerWave * 4; ++i) {
-      part[i] = vpart[i] = 0.0f;
-      const int byte = row_info[i] & 255, channel = 80 * chunk + (row_info[i] >> 8);
-      valid[i] = byte < nbytes && channel < a.I;
-      expert_row[i] = valid[i] ? (byte % 2) * a.I + channel : 0;
+    for (int k = 0; k < 2; ++k) {
+      const int item = tid + 256 * k;
+      if (item < kMaxSpan * kChunkRows) {
+        sh.scale[item / kChunkRows][item % kChunkRows] = static_cast<uint16_t>(staged.rows[k]);
+        if (kGh5)
+          sh.residual[item / kChunkRows][item % kChunkRows] =
+              static_cast<uint16_t>(staged.rows[k] >> 16);
+      }
     }
-    int8_t *tr = trits();
-    const int pp = lane % 16;
+    __syncthreads();  // (B)
+    // decode: item = (slot group g, code word jw) -> 4 byte columns x 5 digits
+    {
+      const int g = tid % 32, jw = tid / 32;
+#pragma unroll
+      for (int bl = 0; bl < kMaxSpan; ++bl) {
+        const int G = sh.union_groups[bl];
+        if (bl >= blocks || g >= G || 4 * jw >= nbytes) continue;
+        uint32_t word[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) word[i] = sh.raw[bl][(g + G * i) * kRawStride + jw];
+        int8_t *out = trits(bl) + 4 * g;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = 4 * jw + jj;
+          if (j >= nbytes) break;
+          uint2 code[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) code[i] = sh.lut[(word[i] >> (8 * jj)) & 255u];
+          int8_t *row = out + 5 * j * kTritStride;
+#pragma unroll
+          for (int d = 0; d < 4; ++d)
+            *reinterpret_cast<uint32_t *>(row + d * kTritStride) =
+                gather_byte(code[0].x, code[1].x, code[2].x, code[3].x, d);
+          *reinterpret_cast<uint32_t *>(row + 4 * kTritStride) =
+              gather_byte(code[0].y, code[1].y, code[2].y, code[3].y, 0);
+        }
+      }
+    }
+    __syncthreads();  // (C)
+    float part[kTilesPerWave * 4], vpart[kTilesPerWave * 4];
+#pragma unroll
+    for (int i = 0; i < kTilesPerWave * 4; ++i) part[i] = vpart[i] = 0.0f;
+    const int pp = lane % 16, k0 = 16 * (lane / 16);
     for (int bl = 0; bl < blocks; ++bl) {
-      const int U = sh.union_count[bl];
-      const uint32_t *rw = raw(bl);
+      const int columns = 4 * sh.union_groups[bl];
+      const int8_t *tr = trits(bl);
       v4i acc[kTilesPerWave][3];
 #pragma unroll
       for (int ti = 0; ti < kTilesPerWave; ++ti)
 #pragma unroll
         for (int d = 0; d < 3; ++d) acc[ti][d] = v4i{0, 0, 0, 0};
-      for (int half = 0; half * kHalfCoords < U; ++half) {
-        __syncthreads();
-        // decode: byte column j of 4 consecutive union positions -> 5 trit rows
+      for (int half = 0; half * kHalfCoords < columns; ++half) {
+        v4i bv[3];
 #pragma unroll
-        for (int round = 0; round < 2; ++round) {
-          const int item = tid + 256 * round;
-          // a wave covers 8 coordinate groups x 8 byte columns
-          const int u4 = (item % 8) + 8 * ((item / 64) % 2);
-          const int j = (item / 8) % 8 + 8 * (item / 128);
-          if (j >= nbytes) continue;
-          const int u0 = half * kHalfCoords + u4 * 4;
-          uint32_t lo[4], hi[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t word = rw[(u0 + i) * kRawStride + j / 4];
-            const uint32_t code = (word >> (8 * (j % 4))) & 255u;
-            lo[i] = sh.lut[code][0];
-            hi[i] = sh.lut[code][1];
-          }
-          int8_t *out = &tr[j * 5 * kTritStride + u4 * 4];
-#pragma unroll
-          for (int d = 0; d < 4; ++d)
-            *reinterpret_cast<uint32_t *>(out + d * kTritStride) =
-                gather_byte(lo[0], lo[1], lo[2], lo[3], d);
-          *reinterpret_cast<uint32_t *>(out + 4 * kTritStride) =
-              gather_byte(hi[0], hi[1], hi[2], hi[3], 0);
-        }
-        __syncthreads();
+        for (int d = 0; d < 3; ++d)
+          bv[d] = *reinterpret_cast<const v4i *>(
+              &sh.digits[bl][(d * kPairTile + pp) * kDigitStride + half * kHalfCoords + k0]);
 #pragma unroll
         for (int ti = 0; ti < kTilesPerWave; ++ti) {
           const int tile = wave + 4 * ti;
           if (tile >= kRowTiles) break;
-          const int k0 = 16 * (lane / 16);
-          const v4i av =
-              *reinterpret_cast<const v4i *>(&tr[(tile * 16 + lane % 16) * kTritStride + k0]);
+          const v4i av = *reinterpret_cast<const v4i *>(
+              &tr[(tile * 16 + pp) * kTritStride + half * kHalfCoords + k0]);
 #pragma unroll
-          for (int d = 0; d < 3; ++d) {
-            const v4i bv = *reinterpret_cast<const v4i *>(
-                &sh.digits[bl][(d * kPairTile + pp) * kDigitStride + half * kHalfCoords + k0]);
-            acc[ti][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, acc[ti][d], 0, 0, 0);
-          }
+          for (int d = 0; d < 3; ++d)
+            acc[ti][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[d], acc[ti][d], 0, 0, 0);
         }
       }
       if (pp < count) {
@@ -655,14 +702,14 @@ struct ScreenContext {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int i = ti * 4 + r;
+            const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
             const int sum = acc[ti][0][r] + (acc[ti][1][r] << 8) + (acc[ti][2][r] << 16);
             const float dot = ldexpf(static_cast<float>(sum), -shift);
-            const float sc =
-                static_cast<float>(__builtin_bit_cast(_Float16, sh.scale[bl][expert_row[i]]));
+            const float sc = static_cast<float>(__builtin_bit_cast(_Float16, sh.scale[bl][row]));
             part[i] = fmaf(dot, sc, part[i]);
-            if (a.gh5) {
-              const float rs = static_cast<float>(
-                  __builtin_bit_cast(_Float16, sh.residual[bl][expert_row[i]]));
+            if (kGh5) {
+              const float rs =
+                  static_cast<float>(__builtin_bit_cast(_Float16, sh.residual[bl][row]));
               vpart[i] = fmaf(rs, norm2, vpart[i]);
             }
           }
@@ -679,17 +726,21 @@ struct ScreenContext {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = ti * 4 + r;
-          if (!valid[i]) continue;
-          const long address = base + (row_info[i] & 1) * a.N + 80 * chunk + (row_info[i] >> 8);
+          const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
+          const int byte = row / 5, channel = 80 * chunk + 5 * (byte / 2) + row % 5;
+          if (byte >= nbytes || channel >= a.I) continue;
+          const long address = base + (byte & 1) * a.N + channel;
           a.parts[address] = part[i];
-          if (a.gh5) a.vparts[address] = vpart[i];
+          if (kGh5) a.vparts[address] = vpart[i];
         }
       }
     }
   }
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void group_screen_kernel(GroupScreenArgs a) {
+template <bool kGh5>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void group_screen_kernel(
+    GroupScreenArgs a) {
   __shared__ ScreenShared sh;
   // XCD-aware work order: consecutive work items run on one XCD (workgroups
   // are dealt to the 8 XCDs round-robin), so the chunk groups of one expert
@@ -711,11 +762,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   const int rows2 = 2 * a.I;
   const int b_begin = s * a.span, b_end = min(B, (s + 1) * a.span);
   const int blocks = b_end - b_begin;
-  ScreenContext ctx{a, sh, tid, tid & 63, tid >> 6, e, B, a.stride - a.stride % 32,
+  ScreenContext<kGh5> ctx{a, sh, tid, tid & 63, tid >> 6, e, B, a.stride - a.stride % 32,
                     cg * a.per_group, min(a.per_group, a.chunks - cg * a.per_group),
                     b_begin, blocks, 0, s, a.codes + static_cast<long>(e) * a.storage,
-                    {}, {}};
-  ctx.setup_rows();
+                    {}};
   uint8_t(*staged_coords)[kPairTile][128] =
       reinterpret_cast<uint8_t(*)[kPairTile][128]>(sh.arena);
   uint32_t(*staged_digits)[kPairTile][128] = reinterpret_cast<uint32_t(*)[kPairTile][128]>(
@@ -729,25 +779,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       if (d < 4) lo |= t8 << (8 * d); else hi = t8;
       value /= 3;
     }
-    sh.lut[tid][0] = lo;
-    sh.lut[tid][1] = hi;
+    sh.lut[tid] = make_uint2(lo, hi);
   }
-  // The expert's FP16 scale (and residual) rows of the chunk range's gate and
-  // up channels, for the split's blocks (channel counts are even).
-  {
-    const int channel_begin = 80 * ctx.c_begin;
-    const int channel_end = min(a.I, 80 * (ctx.c_begin + ctx.c_count));
-    const int words = (channel_end - channel_begin) / 2;
-    for (int item = tid; item < blocks * 2 * words; item += 256) {
-      const int bl = item / (2 * words), rest = item % (2 * words);
-      const int r2 = ((rest / words) * a.I + channel_begin) / 2 + rest % words;
-      const uint32_t *plane = reinterpret_cast<const uint32_t *>(
-          a.stats + (static_cast<long>(e) * B + b_begin + bl) * 2 * rows2);
-      reinterpret_cast<uint32_t *>(sh.scale[bl])[r2] = plane[r2];
-      if (a.gh5) reinterpret_cast<uint32_t *>(sh.residual[bl])[r2] = plane[rows2 / 2 + r2];
-    }
-  }
-
   for (int pair_base = 0; pair_base < members; pair_base += kPairTile) {
     const int count = min(kPairTile, members - pair_base);
     ctx.count = count;
@@ -790,8 +823,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       for (int w = 0; w < word; ++w) before += __popc(sh.mask[bl][w]);
       before += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
       if ((sh.mask[bl][word] >> bit) & 1u) sh.union_list[bl][before] = static_cast<uint8_t>(c);
-      if (c == 127) sh.union_count[bl] = before + ((sh.mask[bl][word] >> bit) & 1u);
+      if (c == 127) {
+        const int union_count = before + ((sh.mask[bl][word] >> bit) & 1u);
+        sh.union_count[bl] = union_count;
+        sh.union_groups[bl] = (union_count + 3) / 4;
+      }
     }
+    __syncthreads();
     for (int item = tid; item < blocks * count * keep; item += 256) {
       const int bl = item / (count * keep), rest = item % (count * keep);
       const int pp = rest / keep, j = rest % keep;
@@ -801,33 +839,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       for (int w = 0; w < word; ++w) u += __popc(sh.mask[bl][w]);
       u += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
       const uint32_t packed = staged_digits[bl][pp][j];
-      sh.digits[bl][(0 * kPairTile + pp) * kDigitStride + u] = static_cast<int8_t>(packed & 255u);
-      sh.digits[bl][(1 * kPairTile + pp) * kDigitStride + u] =
+      const int column = union_column(u, sh.union_groups[bl]);
+      sh.digits[bl][(0 * kPairTile + pp) * kDigitStride + column] =
+          static_cast<int8_t>(packed & 255u);
+      sh.digits[bl][(1 * kPairTile + pp) * kDigitStride + column] =
           static_cast<int8_t>((packed >> 8) & 255u);
-      sh.digits[bl][(2 * kPairTile + pp) * kDigitStride + u] =
+      sh.digits[bl][(2 * kPairTile + pp) * kDigitStride + column] =
           static_cast<int8_t>((packed >> 16) & 255u);
     }
     __syncthreads();
 
     ctx.setup_fetch();
-    uint32_t ring0[kMaxSpan][kWordsPerThread], ring1[kMaxSpan][kWordsPerThread];
-    uint32_t ring2[kMaxSpan][kWordsPerThread], ring3[kMaxSpan][kWordsPerThread];
+    Staged ring0, ring1;
     ctx.fetch(0, ring0);
     ctx.fetch(1, ring1);
-    ctx.fetch(2, ring2);
-    ctx.fetch(3, ring3);
     for (int ci = 0; ci < ctx.c_count; ci += kRing) {
       ctx.process(ci, ring0);
       ctx.fetch(ci + kRing, ring0);
       if (ci + 1 >= ctx.c_count) break;
       ctx.process(ci + 1, ring1);
       ctx.fetch(ci + 1 + kRing, ring1);
-      if (ci + 2 >= ctx.c_count) break;
-      ctx.process(ci + 2, ring2);
-      ctx.fetch(ci + 2 + kRing, ring2);
-      if (ci + 3 >= ctx.c_count) break;
-      ctx.process(ci + 3, ring3);
-      ctx.fetch(ci + 3 + kRing, ring3);
     }
   }
 }
@@ -1639,8 +1670,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     const long items =
         groups_bound * s.splits * ((sc.chunks + sc.per_group - 1) / sc.per_group);
     if (stages & (1u << CFMOE_STAGE_SCREEN)) {
-      hipLaunchKernelGGL(group_screen_kernel, dim3(static_cast<unsigned>(items)), dim3(256), 0,
-                         stream, sc);
+      if (gh5)
+        hipLaunchKernelGGL(group_screen_kernel<true>, dim3(static_cast<unsigned>(items)),
+                           dim3(256), 0, stream, sc);
+      else
+        hipLaunchKernelGGL(group_screen_kernel<false>, dim3(static_cast<unsigned>(items)),
+                           dim3(256), 0, stream, sc);
       if ((rc = check_launch("screen"))) return rc;
     }
 
