@@ -432,14 +432,13 @@ struct GroupScreenArgs {
   float *parts;
   float *vparts;
   long storage;
-  int H, I, K, N, keep, stride, splits, span, chunks, per_group, gh5;
+  int H, I, K, N, keep, stride, splits, span, chunks, gh5;
 };
 
 constexpr int kChunkBytes = 32;
 constexpr int kChunkRows = 5 * kChunkBytes;  // 160
 constexpr int kRowTiles = kChunkRows / 16;   // 10
 constexpr int kPairTile = 16;
-constexpr int kResidentScreenGroups = 512;  // 256 CUs x 2 workgroups (LDS, VGPRs)
 static_assert(kPairTile == kGroupPairs, "a screen workgroup holds one grouping tile");
 constexpr int kCoordStride = 128;            // union slots per block
 // LDS row strides, padded so that the lanes of a wave spread over the banks
@@ -635,31 +634,35 @@ struct ScreenContext {
       }
     }
     __syncthreads();  // (B)
-    // decode: item = (slot group g, code word jw) -> 4 byte columns x 5 digits
+    // decode: item = (slot group g, code word jw) -> 4 byte columns x 5 digits.
+    // Branch-free so that all LDS reads issue together: items past the union
+    // (g >= G), past the chunk's bytes or of an absent second block write
+    // trit rows or columns that no MFMA output uses (zero digits or rows that
+    // are never stored); every index stays inside the tiles.
     {
       const int g = tid % 32, jw = tid / 32;
 #pragma unroll
       for (int bl = 0; bl < kMaxSpan; ++bl) {
-        const int G = sh.union_groups[bl];
-        if (bl >= blocks || g >= G || 4 * jw >= nbytes) continue;
+        const int G = max(sh.union_groups[bl], 1);
         uint32_t word[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) word[i] = sh.raw[bl][(g + G * i) * kRawStride + jw];
-        int8_t *out = trits(bl) + 4 * g;
+        for (int i = 0; i < 4; ++i)
+          word[i] = sh.raw[bl][min(g + G * i, kCoordStride - 1) * kRawStride + jw];
+        uint2 code[4][4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) code[jj][i] = sh.lut[(word[i] >> (8 * jj)) & 255u];
+        int8_t *out = trits(bl) + 4 * g + 20 * jw * kTritStride;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const int j = 4 * jw + jj;
-          if (j >= nbytes) break;
-          uint2 code[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) code[i] = sh.lut[(word[i] >> (8 * jj)) & 255u];
-          int8_t *row = out + 5 * j * kTritStride;
+          int8_t *row = out + 5 * jj * kTritStride;
 #pragma unroll
           for (int d = 0; d < 4; ++d)
             *reinterpret_cast<uint32_t *>(row + d * kTritStride) =
-                gather_byte(code[0].x, code[1].x, code[2].x, code[3].x, d);
+                gather_byte(code[jj][0].x, code[jj][1].x, code[jj][2].x, code[jj][3].x, d);
           *reinterpret_cast<uint32_t *>(row + 4 * kTritStride) =
-              gather_byte(code[0].y, code[1].y, code[2].y, code[3].y, 0);
+              gather_byte(code[jj][0].y, code[jj][1].y, code[jj][2].y, code[jj][3].y, 0);
         }
       }
     }
@@ -719,7 +722,8 @@ struct ScreenContext {
     // store this chunk's split partial projections
     if (pp < count) {
       const int t = sh.pair_token[pp], slot = sh.pair_slot[pp];
-      const long base = (static_cast<long>(t) * a.splits + s) * 2 * a.N + slot * a.I;
+      float *parts = a.parts + (static_cast<long>(t) * a.splits + s) * 2 * a.N + slot * a.I;
+      float *vparts = kGh5 ? a.vparts + (parts - a.parts) : nullptr;
 #pragma unroll
       for (int ti = 0; ti < kTilesPerWave; ++ti) {
         if (wave + 4 * ti >= kRowTiles) break;
@@ -729,134 +733,146 @@ struct ScreenContext {
           const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
           const int byte = row / 5, channel = 80 * chunk + 5 * (byte / 2) + row % 5;
           if (byte >= nbytes || channel >= a.I) continue;
-          const long address = base + (byte & 1) * a.N + channel;
-          a.parts[address] = part[i];
-          if (kGh5) a.vparts[address] = vpart[i];
+          const int offset = (byte & 1) * a.N + channel;
+          parts[offset] = part[i];
+          if (kGh5) vparts[offset] = vpart[i];
         }
       }
     }
   }
 };
 
+// Stage a tile's pairs for the split's blocks: kept coordinates, their union
+// per block and the grid digits in union-column order.
 template <bool kGh5>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void group_screen_kernel(
-    GroupScreenArgs a) {
-  __shared__ ScreenShared sh;
-  // XCD-aware work order: consecutive work items run on one XCD (workgroups
-  // are dealt to the 8 XCDs round-robin), so the chunk groups of one expert
-  // block share that XCD's L2.
-  const int total = gridDim.x, p = blockIdx.x;
-  const int per = total / 8, extra = total % 8, xcd = p % 8;
-  const int work = xcd * per + min(xcd, extra) + p / 8;
-  const int groups_per_split = (a.chunks + a.per_group - 1) / a.per_group;
-  const int cg = work % groups_per_split;
-  const int s = (work / groups_per_split) % a.splits;
-  const int z = work / (groups_per_split * a.splits);
-  if (z >= *a.group_total) return;
+__device__ void stage_tile(const GroupScreenArgs &a, ScreenShared &sh, int z, int b_begin,
+                           int blocks, int &count) {
   const int tid = threadIdx.x;
-  const int e = a.group_experts[z];
-  const int members = a.group_counts[z];
-  const int first_pair = a.group_starts[z];
   const int B = a.H / 128;
   const int keep = a.keep;
-  const int rows2 = 2 * a.I;
-  const int b_begin = s * a.span, b_end = min(B, (s + 1) * a.span);
-  const int blocks = b_end - b_begin;
-  ScreenContext<kGh5> ctx{a, sh, tid, tid & 63, tid >> 6, e, B, a.stride - a.stride % 32,
-                    cg * a.per_group, min(a.per_group, a.chunks - cg * a.per_group),
-                    b_begin, blocks, 0, s, a.codes + static_cast<long>(e) * a.storage,
-                    {}};
+  const int first_pair = a.group_starts[z];
+  count = a.group_counts[z];
   uint8_t(*staged_coords)[kPairTile][128] =
       reinterpret_cast<uint8_t(*)[kPairTile][128]>(sh.arena);
   uint32_t(*staged_digits)[kPairTile][128] = reinterpret_cast<uint32_t(*)[kPairTile][128]>(
       sh.arena + ScreenShared::kStageCoordBytes);
+  __syncthreads();  // the previous segment's tiles and digits are consumed
+  if (tid < count) {
+    const int pair = a.group_pairs[first_pair + tid];
+    sh.pair_token[tid] = pair / a.K;
+    sh.pair_slot[tid] = pair % a.K;
+  }
+  if (tid < kMaxSpan * 4) sh.mask[tid / 4][tid % 4] = 0;
+  __syncthreads();
+  for (int item = tid; item < blocks * count * keep; item += 256) {
+    const int bl = item / (count * keep), rest = item % (count * keep);
+    const int pp = rest / keep, j = rest % keep;
+    const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
+    const int coord = keep < 128 ? a.coords[cell * keep + j] : j;
+    int d0, d1, d2;
+    grid_digits(a.qvals[cell * keep + j], d0, d1, d2);
+    staged_coords[bl][pp][j] = static_cast<uint8_t>(coord);
+    staged_digits[bl][pp][j] = (static_cast<uint32_t>(d0) & 255u) |
+                               ((static_cast<uint32_t>(d1) & 255u) << 8) |
+                               ((static_cast<uint32_t>(d2) & 255u) << 16);
+    atomicOr(&sh.mask[bl][coord >> 5], 1u << (coord & 31));
+  }
+  if (tid < blocks * count) {
+    const int bl = tid / count, pp = tid % count;
+    const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
+    sh.pair_shift[bl][pp] = a.qexp[cell];
+    sh.pair_norm2[bl][pp] = kGh5 ? a.norm2[cell] : 0.0f;
+  }
+  for (int i = tid; i < kMaxSpan * 3 * kPairTile * kDigitStride / 16; i += 256)
+    reinterpret_cast<uint4 *>(&sh.digits[0][0])[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  // union lists (ascending coordinates)
+  for (int item = tid; item < blocks * 128; item += 256) {
+    const int bl = item / 128, c = item % 128;
+    const int word = c >> 5, bit = c & 31;
+    int before = 0;
+    for (int w = 0; w < word; ++w) before += __popc(sh.mask[bl][w]);
+    before += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
+    if ((sh.mask[bl][word] >> bit) & 1u) sh.union_list[bl][before] = static_cast<uint8_t>(c);
+    if (c == 127) {
+      const int union_count = before + ((sh.mask[bl][word] >> bit) & 1u);
+      sh.union_count[bl] = union_count;
+      sh.union_groups[bl] = (union_count + 3) / 4;
+    }
+  }
+  if (blocks < kMaxSpan && tid == 0) {
+    sh.union_count[kMaxSpan - 1] = 0;
+    sh.union_groups[kMaxSpan - 1] = 0;
+  }
+  __syncthreads();
+  for (int item = tid; item < blocks * count * keep; item += 256) {
+    const int bl = item / (count * keep), rest = item % (count * keep);
+    const int pp = rest / keep, j = rest % keep;
+    const int coord = staged_coords[bl][pp][j];
+    const int word = coord >> 5, bit = coord & 31;
+    int u = 0;
+    for (int w = 0; w < word; ++w) u += __popc(sh.mask[bl][w]);
+    u += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
+    const uint32_t packed = staged_digits[bl][pp][j];
+    const int column = union_column(u, sh.union_groups[bl]);
+    sh.digits[bl][(0 * kPairTile + pp) * kDigitStride + column] =
+        static_cast<int8_t>(packed & 255u);
+    sh.digits[bl][(1 * kPairTile + pp) * kDigitStride + column] =
+        static_cast<int8_t>((packed >> 8) & 255u);
+    sh.digits[bl][(2 * kPairTile + pp) * kDigitStride + column] =
+        static_cast<int8_t>((packed >> 16) & 255u);
+  }
+  __syncthreads();
+}
 
+// Fixed grid of resident workgroups. The live work is the flattened list of
+// (tile, split, chunk) items, tile-major, whose length is known only on the
+// device (tile count from the grouping); workgroup w takes the contiguous
+// range [w N / grid, (w + 1) N / grid), so every workgroup gets the same
+// number of chunks to within one and restages its tile only where the range
+// crosses a (tile, split) boundary.
+template <bool kGh5>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void group_screen_kernel(
+    GroupScreenArgs a) {
+  __shared__ ScreenShared sh;
+  const int tid = threadIdx.x;
+  const long items = static_cast<long>(*a.group_total) * a.splits * a.chunks;
+  const long lo = items * blockIdx.x / gridDim.x;
+  const long hi = items * (blockIdx.x + 1) / gridDim.x;
+  if (lo >= hi) return;
   {
     int value = tid;
-    uint32_t lo = 0, hi = 0;
+    uint32_t t_lo = 0, t_hi = 0;
     for (int d = 0; d < 5; ++d) {
       const uint32_t t8 = static_cast<uint8_t>(static_cast<int8_t>(value % 3 - 1));
-      if (d < 4) lo |= t8 << (8 * d); else hi = t8;
+      if (d < 4) t_lo |= t8 << (8 * d); else t_hi = t8;
       value /= 3;
     }
-    sh.lut[tid] = make_uint2(lo, hi);
+    sh.lut[tid] = make_uint2(t_lo, t_hi);
   }
-  for (int pair_base = 0; pair_base < members; pair_base += kPairTile) {
-    const int count = min(kPairTile, members - pair_base);
-    ctx.count = count;
-    __syncthreads();
-    if (tid < count) {
-      const int pair = a.group_pairs[first_pair + pair_base + tid];
-      sh.pair_token[tid] = pair / a.K;
-      sh.pair_slot[tid] = pair % a.K;
-    }
-    if (tid < kMaxSpan * 4) sh.mask[tid / 4][tid % 4] = 0;
-    __syncthreads();
-    // Stage every block's kept coordinates and grid digits at once.
-    for (int item = tid; item < blocks * count * keep; item += 256) {
-      const int bl = item / (count * keep), rest = item % (count * keep);
-      const int pp = rest / keep, j = rest % keep;
-      const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
-      const int coord = keep < 128 ? a.coords[cell * keep + j] : j;
-      int d0, d1, d2;
-      grid_digits(a.qvals[cell * keep + j], d0, d1, d2);
-      staged_coords[bl][pp][j] = static_cast<uint8_t>(coord);
-      staged_digits[bl][pp][j] = (static_cast<uint32_t>(d0) & 255u) |
-                                 ((static_cast<uint32_t>(d1) & 255u) << 8) |
-                                 ((static_cast<uint32_t>(d2) & 255u) << 16);
-      atomicOr(&sh.mask[bl][coord >> 5], 1u << (coord & 31));
-    }
-    if (tid < blocks * count) {
-      const int bl = tid / count, pp = tid % count;
-      const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
-      sh.pair_shift[bl][pp] = a.qexp[cell];
-      sh.pair_norm2[bl][pp] = a.gh5 ? a.norm2[cell] : 0.0f;
-    }
-    for (int i = tid; i < blocks * 3 * kPairTile * kDigitStride / 16; i += 256)
-      reinterpret_cast<uint4 *>(&sh.digits[0][0])[i] = make_uint4(0, 0, 0, 0);
-    __syncthreads();
-    // Union lists, then the digit planes in union order.
-    for (int item = tid; item < blocks * 128; item += 256) {
-      const int bl = item / 128, c = item % 128;
-      const int word = c >> 5, bit = c & 31;
-      int before = 0;
-      for (int w = 0; w < word; ++w) before += __popc(sh.mask[bl][w]);
-      before += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
-      if ((sh.mask[bl][word] >> bit) & 1u) sh.union_list[bl][before] = static_cast<uint8_t>(c);
-      if (c == 127) {
-        const int union_count = before + ((sh.mask[bl][word] >> bit) & 1u);
-        sh.union_count[bl] = union_count;
-        sh.union_groups[bl] = (union_count + 3) / 4;
-      }
-    }
-    __syncthreads();
-    for (int item = tid; item < blocks * count * keep; item += 256) {
-      const int bl = item / (count * keep), rest = item % (count * keep);
-      const int pp = rest / keep, j = rest % keep;
-      const int coord = staged_coords[bl][pp][j];
-      const int word = coord >> 5, bit = coord & 31;
-      int u = 0;
-      for (int w = 0; w < word; ++w) u += __popc(sh.mask[bl][w]);
-      u += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
-      const uint32_t packed = staged_digits[bl][pp][j];
-      const int column = union_column(u, sh.union_groups[bl]);
-      sh.digits[bl][(0 * kPairTile + pp) * kDigitStride + column] =
-          static_cast<int8_t>(packed & 255u);
-      sh.digits[bl][(1 * kPairTile + pp) * kDigitStride + column] =
-          static_cast<int8_t>((packed >> 8) & 255u);
-      sh.digits[bl][(2 * kPairTile + pp) * kDigitStride + column] =
-          static_cast<int8_t>((packed >> 16) & 255u);
-    }
-    __syncthreads();
-
+  const int B = a.H / 128;
+  for (long index = lo; index < hi;) {
+    const long segment = index / a.chunks;  // (tile, split)
+    const int c_begin = static_cast<int>(index % a.chunks);
+    const int c_count = static_cast<int>(min(static_cast<long>(a.chunks - c_begin), hi - index));
+    index += c_count;
+    const int z = static_cast<int>(segment / a.splits);
+    const int s = static_cast<int>(segment % a.splits);
+    const int e = a.group_experts[z];
+    const int b_begin = s * a.span, blocks = min(B, (s + 1) * a.span) - b_begin;
+    int count;
+    stage_tile<kGh5>(a, sh, z, b_begin, blocks, count);
+    ScreenContext<kGh5> ctx{a, sh, tid, tid & 63, tid >> 6, e, B, a.stride - a.stride % 32,
+                            c_begin, c_count, b_begin, blocks, count, s,
+                            a.codes + static_cast<long>(e) * a.storage, {}};
     ctx.setup_fetch();
     Staged ring0, ring1;
     ctx.fetch(0, ring0);
     ctx.fetch(1, ring1);
-    for (int ci = 0; ci < ctx.c_count; ci += kRing) {
+    for (int ci = 0; ci < c_count; ci += kRing) {
       ctx.process(ci, ring0);
       ctx.fetch(ci + kRing, ring0);
-      if (ci + 1 >= ctx.c_count) break;
+      if (ci + 1 >= c_count) break;
       ctx.process(ci + 1, ring1);
       ctx.fetch(ci + 1 + kRing, ring1);
     }
@@ -1408,6 +1424,23 @@ __global__ __launch_bounds__(256) void output_kernel(OutputArgs a) {
 
 thread_local char g_error[512] = "";
 
+// Screen workgroups per launch: two resident per CU (LDS and VGPR budget),
+// from the current device's CU count (cached per device).
+long screen_workgroups() {
+  static int cached[64] = {};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 512;
+  if (cached[device] == 0) {
+    int units = 0;
+    if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) !=
+            hipSuccess ||
+        units <= 0)
+      units = 256;
+    cached[device] = 2 * units;
+  }
+  return cached[device];
+}
+
 int fail(int code, const char *message) {
   snprintf(g_error, sizeof(g_error), "%s", message);
   return code;
@@ -1651,24 +1684,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     sc.span = s.span;
     sc.chunks = (sc.stride + kChunkBytes - 1) / kChunkBytes;
     sc.gh5 = gh5;
-    // tiles of at most kGroupPairs pairs per touched expert
-    const long pairs = static_cast<long>(tokens) * s.K;
-    const long touched = pairs < dims->experts ? pairs : dims->experts;
-    const long groups_bound =
-        pairs < touched + pairs / kGroupPairs ? pairs : touched + pairs / kGroupPairs;
-    // Several chunks per workgroup amortise the union and digit setup once
-    // experts hold several pairs; small batches spread chunks over as many
-    // workgroups as stay resident at once (two per CU).
-    sc.per_group = sc.chunks;
-    if (tokens < 8) {
-      sc.per_group = 1;
-      while (sc.per_group < sc.chunks &&
-             groups_bound * s.splits * ((sc.chunks + sc.per_group - 1) / sc.per_group) >
-                 kResidentScreenGroups)
-        ++sc.per_group;
-    }
-    const long items =
-        groups_bound * s.splits * ((sc.chunks + sc.per_group - 1) / sc.per_group);
+    const long items = screen_workgroups();
     if (stages & (1u << CFMOE_STAGE_SCREEN)) {
       if (gh5)
         hipLaunchKernelGGL(group_screen_kernel<true>, dim3(static_cast<unsigned>(items)),
