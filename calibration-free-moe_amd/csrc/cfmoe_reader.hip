@@ -520,9 +520,16 @@ __device__ __forceinline__ T load_global(const T *p) {
       reinterpret_cast<uintptr_t>(p));
 }
 
+__device__ __forceinline__ uint4 load_global(const uint4 *p) {
+  const u32x4 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(
+      reinterpret_cast<uintptr_t>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Load sources of dead lanes (no branch around a load, no select after it).
 __device__ const uint32_t kZeroCodeWord = 0x79797979u;  // four zero-trit bytes
 __device__ const uint16_t kZeroHalves[2] = {0, 0};
+__device__ const uint4 kZeroVector = {0, 0, 0, 0};
 
 // One chunk's loads in flight: code words of every block and the chunk's
 // FP16 scale | residual << 16 rows (2 per thread).
@@ -1179,6 +1186,119 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
   }
 }
 
+// Grouped exact rows (batches of kGroupExactTokens or more, as
+// progressive.py:2655-2718): wave = (16-pair expert tile, channel). One
+// ballot over the tile's pairs finds those that kept the channel; if any did,
+// the channel's gate and up rows are read once and dotted with each such
+// pair's hidden row in the lane order of exact_kernel (identical results).
+// Workgroups past the tiles (one per token) write the zero results of padded
+// tokens and non-local slots, which the grouping leaves out.
+struct GroupExactArgs {
+  const uint16_t *gate_up;
+  const uint16_t *x;
+  const uint8_t *padding;
+  const int32_t *ids;
+  const int32_t *next_ids;
+  const int32_t *counts;
+  const int32_t *starts;
+  const uint8_t *selected;
+  const int32_t *group_experts;
+  const int32_t *group_starts;
+  const int32_t *group_counts;
+  const int32_t *group_pairs;
+  const int32_t *group_total;
+  float *partial;
+  uint16_t *activations;
+  uint8_t *completed;
+  int H, I, K, N, F, T, gelu, channel_groups, tile_items;
+};
+
+constexpr int kMaxHidden = 2048;
+
+__device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, int logical,
+                                              float g, float u) {
+  const long address = static_cast<long>(t) * 2 * a.N + logical;
+  a.partial[address] = g;
+  a.partial[address + a.N] = u;
+  const float act = bfr(cfm_activate(bfr(g), a.gelu != 0));
+  a.activations[static_cast<long>(t) * a.N + logical] = f2bf(act * bfr(u));
+  a.completed[static_cast<long>(t) * a.N + logical] = 1;
+}
+
+__global__ __launch_bounds__(256) void group_exact_kernel(GroupExactArgs a) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (static_cast<int>(blockIdx.x) >= a.tile_items) {
+    // zero results of a padded token or of a slot with no local expert
+    const int t = blockIdx.x - a.tile_items;
+    if (t >= a.T) return;
+    const bool active = is_active(a.padding, t);
+    for (int k = 0; k < a.K; ++k) {
+      if (active && a.ids[t * a.K + k] >= 0) continue;
+      const int start = a.starts[t * a.K + k], count = a.counts[t * a.K + k];
+      for (int j = tid; j < count && start + j < a.F; j += 256) {
+        const int logical = a.next_ids[static_cast<long>(t) * a.F + start + j];
+        if (logical >= 0 && logical < a.N) exact_results(a, t, logical, 0.0f, 0.0f);
+      }
+    }
+    return;
+  }
+  const int z = blockIdx.x / a.channel_groups;
+  const int c = (blockIdx.x % a.channel_groups) * 4 + wave;
+  if (z >= *a.group_total || c >= a.I) return;
+  const int e = a.group_experts[z], count = a.group_counts[z], first = a.group_starts[z];
+  // lane p < count: pair p of the tile
+  int token = 0, logical = 0;
+  bool kept = false;
+  if (lane < count) {
+    const int pair = a.group_pairs[first + lane];
+    token = pair / a.K;
+    logical = (pair % a.K) * a.I + c;
+    kept = a.selected[static_cast<long>(token) * a.N + logical] != 0;
+  }
+  const uint64_t mask = __ballot(kept);
+  if (!mask) return;
+  const uint16_t *grow = a.gate_up + (static_cast<long>(e) * 2 * a.I + c) * a.H;
+  const uint16_t *urow = grow + static_cast<long>(a.I) * a.H;
+  constexpr int kParts = kMaxHidden / 512;
+  uint4 gw[kParts], uw[kParts];
+#pragma unroll
+  for (int j = 0; j < kParts; ++j) {
+    const int h = min(512 * j + 8 * lane, a.H - 8);
+    gw[j] = load_stream16(grow + h);
+    uw[j] = load_stream16(urow + h);
+  }
+  for (uint64_t rest = mask; rest; rest &= rest - 1) {
+    const int pp = __builtin_ctzll(rest);
+    const int t = __shfl(token, pp);
+    const int target = __shfl(logical, pp);
+    const uint16_t *xr = a.x + static_cast<long>(t) * a.H;
+    float g = 0.0f, uu = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kParts; ++j) {
+      const int h = 512 * j + 8 * lane;
+      if (h >= a.H) continue;
+      const uint4 xw = *reinterpret_cast<const uint4 *>(xr + h);
+      const uint32_t gv[4] = {gw[j].x, gw[j].y, gw[j].z, gw[j].w};
+      const uint32_t uv[4] = {uw[j].x, uw[j].y, uw[j].z, uw[j].w};
+      const uint32_t xv[4] = {xw.x, xw.y, xw.z, xw.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
+        g = fmaf(__uint_as_float(gv[i] << 16), x0, g);
+        g = fmaf(__uint_as_float(gv[i] & 0xffff0000u), x1, g);
+        uu = fmaf(__uint_as_float(uv[i] << 16), x0, uu);
+        uu = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, uu);
+      }
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+      g = g + __shfl_xor(g, m);
+      uu = uu + __shfl_xor(uu, m);
+    }
+    if (lane == 0) exact_results(a, t, target, g, uu);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // encode (progressive.py:1859-1951): skipped channels of a 64-channel tile
 
@@ -1317,30 +1437,28 @@ struct OutputArgs {
 };
 
 constexpr int kMaxSlots = 64;        // top_k limit of the C-ABI
+constexpr int kGroupExactTokens = 16;  // batches that use group_exact_kernel
 constexpr int kMaxRank = 64;         // recovery rank limit of the C-ABI
 constexpr int kOutputColumns = 64;   // outputs per workgroup
-constexpr int kOutputStage = 32;     // down tiles staged in LDS per phase
+constexpr int kOutputThreads = 512;
 constexpr int kMaxEncoderTiles = 16; // ceil(I / 64) at I <= 1024
+constexpr int kTileBatch = 8;        // tile partials loaded together per thread
 
-// Workgroup = 64 outputs of one token. All loads of a phase are issued
-// together (staged through LDS); one wave then walks the sums in the fixed
-// order: tiles of a slot in order, slots in order.
-__global__ __launch_bounds__(256) void output_kernel(OutputArgs a) {
+// Workgroup = 64 outputs of one token, 512 threads. Thread (slot k, output)
+// sums the slot's 16-channel tile partials in tile order (all loads of a
+// batch issued together) and rounds to BF16; 64 threads then mix the slots
+// in order with the router weights and add the decoder correction.
+__global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   __shared__ float slot_latent[kMaxSlots * kMaxRank];
   __shared__ float latent[kMaxRank];
-  __shared__ float staged[kOutputStage][kOutputColumns];
-  __shared__ int slot_first[kMaxSlots], slot_tiles[kMaxSlots];
+  __shared__ float slot_value[kMaxSlots][kOutputColumns];
   __shared__ float slot_weight[kMaxSlots];
   const int t = blockIdx.y, tid = threadIdx.x;
   const int o0 = blockIdx.x * kOutputColumns;
   const int K = a.K, R = a.R;
-  for (int k = tid; k < K; k += 256) {
-    slot_first[k] = a.down_tile_starts[t * K + k];
-    slot_tiles[k] = (a.counts[t * K + k] + 15) / 16;
-    slot_weight[k] = a.weights[t * K + k];
-  }
+  for (int k = tid; k < K; k += kOutputThreads) slot_weight[k] = a.weights[t * K + k];
   // each slot's encoder tiles summed in tile order, rounded to BF16
-  for (int item = tid; item < K * R; item += 256) {
+  for (int item = tid; item < K * R; item += kOutputThreads) {
     const int k = item / R, r = item % R;
     const float *parts = a.encoder_parts + (static_cast<long>(t) * K + k) * a.encoder_tiles * R + r;
     float v[kMaxEncoderTiles];
@@ -1352,6 +1470,26 @@ __global__ __launch_bounds__(256) void output_kernel(OutputArgs a) {
       if (j < a.encoder_tiles) total = total + v[j];
     slot_latent[k * R + r] = bfr(total);
   }
+  // each slot's down tiles summed in tile order, rounded to BF16
+  for (int item = tid; item < K * kOutputColumns; item += kOutputThreads) {
+    const int k = item / kOutputColumns, column = item % kOutputColumns;
+    const int o = o0 + column;
+    const int first = a.down_tile_starts[t * K + k];
+    const int tiles = min((a.counts[t * K + k] + 15) / 16, a.max_tiles - first);
+    const float *parts = a.down_parts + (static_cast<long>(t) * a.max_tiles + first) * a.H +
+                         min(o, a.H - 1);
+    float total = 0.0f;
+    for (int j0 = 0; j0 < tiles; j0 += kTileBatch) {
+      float v[kTileBatch];
+#pragma unroll
+      for (int j = 0; j < kTileBatch; ++j)
+        v[j] = parts[static_cast<long>(min(j0 + j, tiles - 1)) * a.H];
+#pragma unroll
+      for (int j = 0; j < kTileBatch; ++j)
+        if (j0 + j < tiles) total = j0 + j == 0 ? v[j] : total + v[j];
+    }
+    slot_value[k][column] = bfr(total);
+  }
   __syncthreads();
   if (tid < R) {
     float mixed = 0.0f;
@@ -1359,40 +1497,11 @@ __global__ __launch_bounds__(256) void output_kernel(OutputArgs a) {
     latent[tid] = mixed;
     if (blockIdx.x == 0) a.latent[static_cast<long>(t) * R + tid] = mixed;
   }
-  int needed = 0;
-  for (int k = 0; k < K; ++k) needed = max(needed, slot_first[k] + slot_tiles[k]);
-  needed = min(needed, a.max_tiles);
+  __syncthreads();
   const int o = o0 + tid;
-  int k = 0, j = 0;
-  float total = 0.0f, routed = 0.0f;
-  const float *parts = a.down_parts + static_cast<long>(t) * a.max_tiles * a.H + o0;
-  for (int base = 0; base < needed; base += kOutputStage) {
-    __syncthreads();
-    for (int item = tid; item < kOutputStage * kOutputColumns; item += 256) {
-      const int g = base + item / kOutputColumns, col = item % kOutputColumns;
-      staged[item / kOutputColumns][col] =
-          (g < needed && o0 + col < a.H) ? parts[static_cast<long>(g) * a.H + col] : 0.0f;
-    }
-    __syncthreads();
-    if (tid < kOutputColumns) {
-      while (k < K) {
-        const int g = slot_first[k] + j;
-        if (j >= slot_tiles[k] || g >= a.max_tiles) {
-          routed = fmaf(bfr(total), slot_weight[k], routed);
-          ++k;
-          j = 0;
-          total = 0.0f;
-          continue;
-        }
-        if (g >= base + kOutputStage) break;
-        const float p = staged[g - base][tid];
-        total = j == 0 ? p : total + p;
-        ++j;
-      }
-    }
-  }
   if (tid >= kOutputColumns || o >= a.H) return;
-  for (; k < K; ++k, j = 0, total = 0.0f) routed = fmaf(bfr(total), slot_weight[k], routed);
+  float routed = 0.0f;
+  for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k][tid], slot_weight[k], routed);
   float correction = 0.0f;
   if (R > 0 && a.decoder) {
     const bool active = is_active(a.padding, t);
@@ -1423,6 +1532,15 @@ __global__ __launch_bounds__(256) void output_kernel(OutputArgs a) {
 // host side
 
 thread_local char g_error[512] = "";
+
+// Upper bound of the grouping's tile count: every touched expert contributes
+// one tile plus one per 16 further pairs.
+long tile_bound(int tokens, int top_k, int experts) {
+  const long pairs = static_cast<long>(tokens) * top_k;
+  const long touched = pairs < experts ? pairs : experts;
+  const long bound = touched + pairs / kGroupPairs;
+  return pairs < bound ? pairs : bound;
+}
 
 // Screen workgroups per launch: two resident per CU (LDS and VGPR budget),
 // from the current device's CU count (cached per device).
@@ -1746,7 +1864,38 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   ex.F = s.F;
   ex.gelu = gelu;
   if (stages & (1u << CFMOE_STAGE_EXACT)) {
-    hipLaunchKernelGGL(exact_kernel, dim3((s.F + 3) / 4, tokens), dim3(256), 0, stream, ex);
+    if (tokens >= kGroupExactTokens) {
+      GroupExactArgs gx;
+      gx.gate_up = ex.gate_up;
+      gx.x = ex.x;
+      gx.padding = padding;
+      gx.ids = workspace->ids;
+      gx.next_ids = workspace->next_ids;
+      gx.counts = workspace->counts;
+      gx.starts = workspace->starts;
+      gx.selected = workspace->selected;
+      gx.group_experts = workspace->group_experts;
+      gx.group_starts = workspace->group_starts;
+      gx.group_counts = workspace->group_counts;
+      gx.group_pairs = workspace->group_pairs;
+      gx.group_total = workspace->group_total;
+      gx.partial = workspace->partial;
+      gx.activations = ex.activations;
+      gx.completed = workspace->completed;
+      gx.H = s.H;
+      gx.I = s.I;
+      gx.K = s.K;
+      gx.N = s.N;
+      gx.F = s.F;
+      gx.T = tokens;
+      gx.gelu = gelu;
+      gx.channel_groups = (s.I + 3) / 4;
+      gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
+      hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + tokens), dim3(256), 0, stream,
+                         gx);
+    } else {
+      hipLaunchKernelGGL(exact_kernel, dim3((s.F + 3) / 4, tokens), dim3(256), 0, stream, ex);
+    }
     if ((rc = check_launch("exact"))) return rc;
   }
 
@@ -1810,7 +1959,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.max_tiles = s.max_tiles;
   op.encoder_tiles = s.encoder_tiles;
   hipLaunchKernelGGL(output_kernel, dim3((s.H + kOutputColumns - 1) / kOutputColumns, tokens),
-                     dim3(256), 0, stream, op);
+                     dim3(kOutputThreads), 0, stream, op);
   return check_launch("output");
 }
 

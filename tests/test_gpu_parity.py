@@ -195,6 +195,34 @@ def test_hot_expert_splits_into_screen_tiles():
     assert sorted(seen) == list(range(tokens * top_k))
 
 
+@pytest.mark.parametrize("score", ["point", "recovery-aware"])
+def test_grouped_batch_paths_bit_exact(score):
+    """Batches of 16 or more use the grouped exact rows and per-slot down
+    values; padded tokens and a non-local slot exercise their zero results."""
+    tokens, experts, top_k = 24, 16, 4
+    layer = make_layer(hidden=512, width=256, experts=experts, top_k=top_k, rank=16,
+                       tokens=tokens, seed=71)
+    layer.ids[5, 2] = 99  # no local expert: reads nothing, contributes zero
+    padding = torch.zeros(tokens, dtype=torch.bool)
+    padding[[3, 10]] = True
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=top_k, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score=score)
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights, padding)
+    assert_parity(reader, out, expected, tokens)
+
+
+def test_grouped_batch_qwen3_shape_bit_exact():
+    tokens = 32
+    layer = make_layer(hidden=2048, width=768, experts=128, top_k=8, rank=32, tokens=tokens,
+                       seed=72)
+    plan = compile_budget(hidden_size=2048, expert_width=768, top_k=8, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+
+
 def test_threshold_selection():
     tokens = 3
     layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=48)
