@@ -31,6 +31,8 @@
 namespace cfmoe {
 
 constexpr int kWave = 64;
+constexpr int kMaxSlots = 64;  // top_k limit of the C-ABI
+constexpr int kMaxRank = 64;   // recovery rank limit of the C-ABI
 
 // ---------------------------------------------------------------------------
 // scalar helpers (identical formulas in oracle/cfmoe_oracle.c)
@@ -127,6 +129,21 @@ __device__ __forceinline__ uint4 load_stream16(const void *address) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Loads through the global address space (global_load, counted by vmcnt
+// only; a generic pointer would make them flat loads that LDS waits also
+// have to drain).
+template <typename T>
+__device__ __forceinline__ T load_global(const T *p) {
+  return *reinterpret_cast<const __attribute__((address_space(1))) T *>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
+__device__ __forceinline__ uint4 load_global(const uint4 *p) {
+  const u32x4 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(
+      reinterpret_cast<uintptr_t>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint64_t lanes_below(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
@@ -211,21 +228,49 @@ __device__ void route_and_group(const PrepareArgs &a) {
   __shared__ __align__(16) int16_t sorted[kMaxPairs];
   __shared__ int16_t routed[kMaxPairs];
   __shared__ int counts[kMaxExperts];
+  __shared__ int segment_count[kPrepareThreads];
+  __shared__ int expert_start[kPrepareThreads], expert_tile[kPrepareThreads];
   __shared__ int scratch[32];
   const int tid = threadIdx.x;
   const int T = a.T, K = a.K;
   const int pairs = T * K;
-  // raw ids (outside [0, E) -> -1: no local expert, reads nothing)
-  for (int p = tid; p < pairs; p += kPrepareThreads) {
-    int id = (a.flags & CFMOE_IDS_INT64)
-                 ? static_cast<int>(static_cast<const int64_t *>(a.router_ids)[p])
-                 : static_cast<const int32_t *>(a.router_ids)[p];
-    routed[p] = static_cast<int16_t>((id < 0 || id >= a.E) ? -1 : id);
+  constexpr int kPerThread = kMaxPairs / kPrepareThreads;
+  // raw ids (outside [0, E) -> -1: no local expert, reads nothing) and each
+  // pair's own router weight, all loads issued together
+  auto weight_of = [&](int q) {
+    return (a.flags & CFMOE_WEIGHTS_BF16)
+               ? bf16f(static_cast<const uint16_t *>(a.router_weights)[q])
+               : static_cast<const float *>(a.router_weights)[q];
+  };
+  // (clamped indices: no branch around the loads, so they issue together)
+  float own_weight[kPerThread];
+  int raw_id[kPerThread];
+  const int rounds = (pairs + kPrepareThreads - 1) / kPrepareThreads;
+#pragma unroll
+  for (int q = 0; q < kPerThread; ++q) {
+    if (q >= rounds) break;
+    const int p = min(tid + kPrepareThreads * q, pairs - 1);
+    raw_id[q] = (a.flags & CFMOE_IDS_INT64)
+                    ? static_cast<int>(load_global(static_cast<const int64_t *>(a.router_ids) + p))
+                    : load_global(static_cast<const int32_t *>(a.router_ids) + p);
+    own_weight[q] =
+        (a.flags & CFMOE_WEIGHTS_BF16)
+            ? bf16f(load_global(static_cast<const uint16_t *>(a.router_weights) + p))
+            : load_global(static_cast<const float *>(a.router_weights) + p);
+  }
+#pragma unroll
+  for (int q = 0; q < kPerThread; ++q) {
+    if (q >= rounds) break;
+    const int p = tid + kPrepareThreads * q;
+    if (p < pairs) routed[p] = static_cast<int16_t>((raw_id[q] < 0 || raw_id[q] >= a.E) ? -1 : raw_id[q]);
   }
   __syncthreads();
   // slot k of a token moves to its rank among the token's ids (ties by slot);
   // its weight is the sum of the weights of equal ids (progressive.py:369-375)
-  for (int p = tid; p < pairs; p += kPrepareThreads) {
+#pragma unroll
+  for (int q = 0; q < kPerThread; ++q) {
+    const int p = tid + kPrepareThreads * q;
+    if (p >= pairs) continue;
     const int t = p / K, k = p % K;
     const bool active = is_active(a.padding, t);
     const int id = routed[p];
@@ -235,15 +280,10 @@ __device__ void route_and_group(const PrepareArgs &a) {
       rank += other < id || (other == id && j < k);
       equal += other == id;
     }
-    auto weight_of = [&](int q) {
-      return (a.flags & CFMOE_WEIGHTS_BF16)
-                 ? bf16f(static_cast<const uint16_t *>(a.router_weights)[q])
-                 : static_cast<const float *>(a.router_weights)[q];
-    };
     float w = 0.0f;
     if (active) {
       if (equal == 1) {
-        w = 0.0f + weight_of(p);
+        w = 0.0f + own_weight[q];
       } else {
         for (int j = 0; j < K; ++j)
           if (routed[t * K + j] == id) w += weight_of(t * K + j);
@@ -256,14 +296,10 @@ __device__ void route_and_group(const PrepareArgs &a) {
   const int padded = (pairs + 7) / 8 * 8;
   for (int p = pairs + tid; p < padded; p += kPrepareThreads) sorted[p] = -1;
   __syncthreads();
-  // thread owns the contiguous experts [first, last)
-  const int span = (a.E + kPrepareThreads - 1) / kPrepareThreads;
-  const int first = min(a.E, tid * span), last = min(a.E, first + span);
-  // an expert's pairs form tiles of at most kGroupPairs (one screen workgroup each)
-  int tiles = 0, members = 0;
-  for (int e = first; e < last; ++e) {
+  // matches of expert e among pairs [begin, end) (multiples of 8)
+  auto matches = [&](int e, int begin, int end) {
     int count = 0;
-    for (int p = 0; p < padded; p += 8) {
+    for (int p = begin; p < end; p += 8) {
       const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -272,34 +308,82 @@ __device__ void route_and_group(const PrepareArgs &a) {
         count += static_cast<int16_t>(w[i] >> 16) == e;
       }
     }
-    counts[e] = count;
-    tiles += (count + kGroupPairs - 1) / kGroupPairs;
-    members += count;
-  }
-  int total_tiles;
-  int z = block_exclusive(tiles, scratch, &total_tiles);
-  int total_members;
-  int start = block_exclusive(members, scratch, &total_members);
-  for (int e = first; e < last; ++e) {
-    const int count = counts[e];
-    if (count == 0) continue;
-    int placed = 0;
-    for (int p = 0; p < padded && placed < count; p += 8) {
+    return count;
+  };
+  // place expert e's pairs among [begin, end) in order from group_pairs[at]
+  auto place = [&](int e, int begin, int end, int at) {
+    for (int p = begin; p < end; p += 8) {
       const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (static_cast<int16_t>(w[i] & 0xffffu) == e) a.group_pairs[start + placed++] = p + 2 * i;
-        if (static_cast<int16_t>(w[i] >> 16) == e) a.group_pairs[start + placed++] = p + 2 * i + 1;
+        if (static_cast<int16_t>(w[i] & 0xffffu) == e) a.group_pairs[at++] = p + 2 * i;
+        if (static_cast<int16_t>(w[i] >> 16) == e) a.group_pairs[at++] = p + 2 * i + 1;
       }
     }
+  };
+  // tiles of at most kGroupPairs pairs, one screen workgroup each
+  auto emit_tiles = [&](int e, int count, int start, int z) {
     for (int first_pair = 0; first_pair < count; first_pair += kGroupPairs) {
       a.group_experts[z] = e;
       a.group_starts[z] = start + first_pair;
       a.group_counts[z] = min(kGroupPairs, count - first_pair);
       ++z;
     }
-    start += count;
+  };
+  int total_tiles;
+  if (a.E <= kPrepareThreads) {
+    // `share` consecutive threads scan consecutive segments of the pairs for
+    // one expert: segment counts, an in-group prefix, ordered placement
+    int share = 1;
+    while (share * 2 * a.E <= kPrepareThreads) share *= 2;
+    const int e = tid / share, part = tid % share;
+    const int segment = (padded / 8 + share - 1) / share * 8;
+    const int begin = min(padded, part * segment), end = min(padded, begin + segment);
+    const int mine = e < a.E ? matches(e, begin, end) : 0;
+    segment_count[tid] = mine;
+    __syncthreads();
+    int before = 0, count = 0;
+    if (e < a.E)
+      for (int j = 0; j < share; ++j) {
+        const int c = segment_count[e * share + j];
+        before += j < part ? c : 0;
+        count += c;
+      }
+    const bool leader = e < a.E && part == 0;
+    int z = block_exclusive(leader ? (count + kGroupPairs - 1) / kGroupPairs : 0, scratch,
+                            &total_tiles);
+    int total_members;
+    const int start = block_exclusive(leader ? count : 0, scratch, &total_members);
+    if (leader) {
+      expert_start[e] = start;
+      expert_tile[e] = z;
+    }
+    __syncthreads();
+    if (e < a.E && mine > 0) place(e, begin, end, expert_start[e] + before);
+    if (leader && count > 0) emit_tiles(e, count, start, z);
+  } else {
+    // each thread owns the contiguous experts [first, last)
+    const int span = (a.E + kPrepareThreads - 1) / kPrepareThreads;
+    const int first = min(a.E, tid * span), last = min(a.E, first + span);
+    int tiles = 0, members = 0;
+    for (int e = first; e < last; ++e) {
+      const int count = matches(e, 0, padded);
+      counts[e] = count;
+      tiles += (count + kGroupPairs - 1) / kGroupPairs;
+      members += count;
+    }
+    int z = block_exclusive(tiles, scratch, &total_tiles);
+    int total_members;
+    int start = block_exclusive(members, scratch, &total_members);
+    for (int e = first; e < last; ++e) {
+      const int count = counts[e];
+      if (count == 0) continue;
+      place(e, 0, padded, start);
+      emit_tiles(e, count, start, z);
+      z += (count + kGroupPairs - 1) / kGroupPairs;
+      start += count;
+    }
   }
   if (tid == 0) *a.group_total = total_tiles;
   // fixed read charges: one add per slot for all active tokens (integers, exact)
@@ -509,21 +593,6 @@ __device__ __forceinline__ uint32_t gather_byte(uint32_t w0, uint32_t w1, uint32
   const uint32_t low = __builtin_amdgcn_perm(w1, w0, select);
   const uint32_t high = __builtin_amdgcn_perm(w3, w2, select);
   return __builtin_amdgcn_perm(high, low, 0x05040100u);
-}
-
-// Loads through the global address space (global_load, counted by vmcnt
-// only; a generic pointer would make them flat loads that LDS waits also
-// have to drain).
-template <typename T>
-__device__ __forceinline__ T load_global(const T *p) {
-  return *reinterpret_cast<const __attribute__((address_space(1))) T *>(
-      reinterpret_cast<uintptr_t>(p));
-}
-
-__device__ __forceinline__ uint4 load_global(const uint4 *p) {
-  const u32x4 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x4 *>(
-      reinterpret_cast<uintptr_t>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // Load sources of dead lanes (no branch around a load, no select after it).
@@ -983,13 +1052,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int t = blockIdx.x, tid = threadIdx.x;
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
+  // keys: every load issued unconditionally (absent keys read a zero)
   uint32_t key[kSelectKeys];
+  const float *row = a.scores + static_cast<long>(t) * a.N;
 #pragma unroll
   for (int j = 0; j < kSelectKeys; ++j) {
-    const int i = first + j;
-    key[j] = (j < per && i < a.N)
-                 ? __float_as_uint(a.scores[static_cast<long>(t) * a.N + i] + 0.0f)
-                 : 0u;
+    const bool present = j < per && first + j < a.N;
+    const float *source =
+        present ? row + first + j : reinterpret_cast<const float *>(&kZeroVector);
+    key[j] = __float_as_uint(load_global(source) + 0.0f);
   }
   auto valid = [&](int j) { return j < per && first + j < a.N; };
   int want = a.F;
@@ -1015,31 +1086,24 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
         if (valid(j) && (key[j] & mask) == prefix)
           atomicAdd(&histogram[(key[j] >> shift) & (bins - 1)], 1);
       __syncthreads();
-      if (tid < 64) {
-        // lane l owns bins [bins - (l + 1) * per_lane, bins - l * per_lane), high first
-        const int per_lane = static_cast<int>(bins) / 64;
-        const int top = static_cast<int>(bins) - tid * per_lane;
-        int mine = 0;
-        for (int i = 1; i <= per_lane; ++i) mine += histogram[top - i];
-        int inclusive = mine;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          int n = __shfl_up(inclusive, o);
-          if (tid >= o) inclusive += n;
-        }
-        const int before = inclusive - mine;
-        const bool crossing = before < want && inclusive >= want;
-        if (crossing) {
-          int running = before;
-          for (int i = 1; i <= per_lane; ++i) {
-            const int h = histogram[top - i];
-            if (running + h >= want) {
-              shared_bin = static_cast<uint32_t>(top - i);
-              shared_above = running;
-              break;
-            }
-            running += h;
+      // thread i owns bins [bins - (i + 1) * per_thread, bins - i * per_thread),
+      // high first; the block scan finds the bin where the count reaches want
+      const int per_thread = static_cast<int>(bins) / kSelectThreads;
+      const int top = static_cast<int>(bins) - tid * per_thread;
+      int mine = 0;
+      for (int i = 1; i <= per_thread; ++i) mine += histogram[top - i];
+      int counted;
+      const int before = block_exclusive(mine, scratch, &counted);
+      if (before < want && before + mine >= want) {
+        int running = before;
+        for (int i = 1; i <= per_thread; ++i) {
+          const int h = histogram[top - i];
+          if (running + h >= want) {
+            shared_bin = static_cast<uint32_t>(top - i);
+            shared_above = running;
+            break;
           }
+          running += h;
         }
       }
       __syncthreads();
@@ -1325,29 +1389,37 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   const long logical = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + c;
   const int e = a.ids[t * a.K + k];
   const bool local = is_active(a.padding, t) && e >= 0;
-  int skip = 0;
+  // every load issued unconditionally (clamped channel, zero row source)
+  const int cc = min(c, a.I - 1);
+  const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + cc;
+  const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + cc;
+  const uint8_t is_selected = load_global(a.selected + flat);
+  const uint8_t is_completed = load_global(a.completed + flat);
+  const uint16_t exact = load_global(a.activations + flat);
+  const float gate = load_global(a.partial + base);
+  const float up = load_global(a.partial + base + a.N);
+  const bool rows16 = (a.R & 7) == 0;
+  uint4 coefficient_rows[kMaxRank / 8];
+  const uint16_t *row = a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + cc) * a.R;
+  if (rows16) {
+#pragma unroll
+    for (int q = 0; q < kMaxRank / 8; ++q) {
+      const uint4 *source = (local && 8 * q < a.R) ? reinterpret_cast<const uint4 *>(row + 8 * q)
+                                                   : &kZeroVector;
+      coefficient_rows[q] = load_global(source);
+    }
+  }
+  const int skip = c < a.I && !is_selected;
   float v = 0.0f;
-  if (c < a.I && !a.selected[logical]) {
-    skip = 1;
-    if (a.completed[logical]) {
-      v = bf16f(a.activations[logical]);
-    } else {
-      const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + c;
-      const float g = bfr(a.partial[base]);
-      const float u = bfr(a.partial[base + a.N]);
-      v = bfr(cfm_activate(g, a.gelu != 0) * u);
-    }
-    // this skipped channel's encoder row: R bf16 (64 B at rank 32)
-    if (local) {
-      const uint16_t *row = a.encoder_t + (static_cast<long>(e) * a.I + c) * a.R;
-      uint16_t *staged = &coefficients[lane * kEncodeStride];
-      if ((a.R & 7) == 0) {
-        for (int q = 0; q < a.R; q += 8)
-          *reinterpret_cast<uint4 *>(staged + q) = load_stream16(row + q);
-      } else {
-        for (int q = 0; q < a.R; ++q) staged[q] = row[q];
-      }
-    }
+  if (skip)
+    v = is_completed ? bf16f(exact) : bfr(cfm_activate(bfr(gate), a.gelu != 0) * bfr(up));
+  uint16_t *staged = &coefficients[lane * kEncodeStride];
+  if (rows16) {
+#pragma unroll
+    for (int q = 0; q < kMaxRank / 8; ++q)
+      if (8 * q < a.R) *reinterpret_cast<uint4 *>(staged + 8 * q) = coefficient_rows[q];
+  } else if (skip && local) {
+    for (int q = 0; q < a.R; ++q) staged[q] = row[q];
   }
   value[lane] = v;
   skipped[lane] = skip;
@@ -1396,23 +1468,45 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   const int e = a.ids[t * a.K + k];
   const bool local = is_active(a.padding, t) && e >= 0;
   const int start = a.starts[t * a.K + k];
+  // the tile's 16 kept positions, a prefix of which is valid (the tile stops
+  // at the count or at the first invalid id); every load is issued
+  // unconditionally from a clamped index or a zero source
+  const int32_t *kept = a.next_ids + static_cast<long>(t) * a.F;
+  int logical[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) logical[j] = load_global(kept + min(start + first + j, a.F - 1));
+  uint32_t live = 0;
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    ok = ok && first + j < count && start + first + j < a.F && logical[j] >= 0 &&
+         logical[j] < a.N;
+    live |= ok ? 1u << j : 0u;
+  }
+  const uint16_t *acts = a.activations + static_cast<long>(t) * a.N;
+  const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + o;
+  float act[16];
+  uint4 w[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const bool use = (live >> j) & 1u;
+    act[j] = bf16f(load_global(acts + (use ? logical[j] : 0)));
+    const uint4 *source = (use && local) ? reinterpret_cast<const uint4 *>(
+                                               rows + static_cast<long>(logical[j] % a.I) * a.H)
+                                         : &kZeroVector;
+    w[j] = load_global(source);
+  }
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
-  for (int j = first; j < first + 16 && j < count; ++j) {
-    if (start + j >= a.F) break;
-    const int logical = a.next_ids[static_cast<long>(t) * a.F + start + j];
-    if (logical < 0 || logical >= a.N) break;
-    const int c = logical % a.I;
-    const float act = bf16f(a.activations[static_cast<long>(t) * a.N + logical]);
-    uint4 w = make_uint4(0, 0, 0, 0);
-    if (local)
-      w = load_stream16(a.down + (static_cast<long>(e) * a.I + c) * a.H + o);
-    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (!((live >> j) & 1u)) break;
+    const uint32_t wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = fmaf(__uint_as_float(wv[i] << 16), act, acc[2 * i]);
-      acc[2 * i + 1] = fmaf(__uint_as_float(wv[i] & 0xffff0000u), act, acc[2 * i + 1]);
+      acc[2 * i] = fmaf(__uint_as_float(wv[i] << 16), act[j], acc[2 * i]);
+      acc[2 * i + 1] = fmaf(__uint_as_float(wv[i] & 0xffff0000u), act[j], acc[2 * i + 1]);
     }
   }
   float *out = a.parts + (static_cast<long>(t) * a.max_tiles + tile) * a.H + o;
@@ -1436,9 +1530,7 @@ struct OutputArgs {
   int H, K, R, max_tiles, encoder_tiles;
 };
 
-constexpr int kMaxSlots = 64;        // top_k limit of the C-ABI
 constexpr int kGroupExactTokens = 16;  // batches that use group_exact_kernel
-constexpr int kMaxRank = 64;         // recovery rank limit of the C-ABI
 constexpr int kOutputColumns = 64;   // outputs per workgroup
 constexpr int kOutputThreads = 512;
 constexpr int kMaxEncoderTiles = 16; // ceil(I / 64) at I <= 1024
