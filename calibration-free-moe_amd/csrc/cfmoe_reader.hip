@@ -188,11 +188,11 @@ __device__ int block_exclusive(int v, int *scratch, int *total) {
 // prepare: route + expert grouping (progressive.py:349-386, :2329-2373) and
 // rotate/mask (:389-453)
 //
-// 256-thread blocks. Wave w of block i rotates cell 4 i + w = (token, block);
-// the wave of a token's block 0 also adds the token's fixed read charges. The
-// last block sorts every token's K ids, then groups the (token, slot) pairs by
-// expert: touched experts in ascending id order, each with its pairs in
-// ascending pair index (deterministic lists, no atomics in the order).
+// 256-thread blocks. Block 0 sorts every token's K ids, groups the (token,
+// slot) pairs by expert into tiles of at most 16 pairs (touched experts in
+// ascending id order, each with its pairs in ascending pair index:
+// deterministic lists, no atomics in the order) and adds the fixed read
+// charges. Wave w of cell block i rotates cell 4 i + w = (token, block).
 
 struct PrepareArgs {
   const uint16_t *x;
@@ -397,15 +397,17 @@ __device__ void route_and_group(const PrepareArgs &a) {
 }
 
 __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
-  if (static_cast<int>(blockIdx.x) * 4 >= a.cells) {
-    if (a.route) route_and_group(a);
+  // block 0 routes and groups (the longest block, dispatched first)
+  if (a.route && blockIdx.x == 0) {
+    route_and_group(a);
     return;
   }
+  const int cell_block = static_cast<int>(blockIdx.x) - (a.route ? 1 : 0);
   __shared__ float compact_all[4][128];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // waves past the last cell still reach the block barrier below
-  const int cell_id = min(static_cast<int>(blockIdx.x) * 4 + wave, a.cells - 1);
-  const bool owner = static_cast<int>(blockIdx.x) * 4 + wave < a.cells;
+  const int cell_id = min(cell_block * 4 + wave, a.cells - 1);
+  const bool owner = cell_block * 4 + wave < a.cells;
   const int B = a.H / 128;
   const int t = cell_id / B, b = cell_id % B;
   float *compact = compact_all[wave];
@@ -648,6 +650,9 @@ struct ScreenContext {
     const bool tail = g0 >= body;
     const bool chunk_live = ci < c_count;
     const int tail_words = (a.stride - g0) / 4;
+    // dead words (no chunk, no coordinate, past the tail) read the chunk's
+    // first word: their values reach only zero-digit columns or unused rows
+    const uint8_t *chunk_codes = expert_codes + (tail ? 0 : g0);
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
       const int b = b_begin + bl;
@@ -656,28 +661,27 @@ struct ScreenContext {
       for (int i = 0; i < kWordsPerThread; ++i) {
         const int info = fetch_info[bl][i];
         const int w = (tid + 256 * i) % 8;
-        const int body_offset = (info & 0xffffff) + g0;
-        const int tail_offset = tail_base + ((info >> 24) & 127) * 32 + 4 * w;
         const bool live = chunk_live && info >= 0 && (!tail || w < tail_words);
-        const uint32_t *source =
-            live ? reinterpret_cast<const uint32_t *>(expert_codes + (tail ? tail_offset : body_offset))
-                 : &kZeroCodeWord;
-        staged.words[bl][i] = load_global(source);
+        const uint32_t offset =
+            live ? static_cast<uint32_t>(tail ? tail_base + ((info >> 24) & 127) * 32 + 4 * w
+                                              : (info & 0xffffff))
+                 : 0u;
+        staged.words[bl][i] =
+            load_global(reinterpret_cast<const uint32_t *>(chunk_codes + offset));
       }
     }
+    // the chunk's FP16 scale (and residual) rows; dead rows read row 0
     const int nbytes = min(kChunkBytes, a.stride - g0);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int item = tid + 256 * k;
-      const int bl = item / kChunkRows, row = item % kChunkRows;
+      const int bl = min(item / kChunkRows, kMaxSpan - 1), row = item % kChunkRows;
       const int j = row / 5, channel = 80 * chunk + 5 * (j / 2) + row % 5;
-      const bool live = chunk_live && bl < blocks && j < nbytes && channel < a.I;
-      const uint16_t *row_source =
-          live ? a.stats + (static_cast<long>(e) * B + b_begin + bl) * 4 * a.I + (j % 2) * a.I +
-                     channel
-               : kZeroHalves;
-      uint32_t value = load_global(row_source);
-      if (kGh5) value |= static_cast<uint32_t>(load_global(row_source + (live ? 2 * a.I : 1))) << 16;
+      const bool live = chunk_live && item < blocks * kChunkRows && j < nbytes && channel < a.I;
+      const uint16_t *plane = a.stats + (static_cast<long>(e) * B + b_begin + min(bl, blocks - 1)) * 4 * a.I;
+      const uint32_t offset = live ? static_cast<uint32_t>((j % 2) * a.I + channel) : 0u;
+      uint32_t value = load_global(plane + offset);
+      if (kGh5) value |= static_cast<uint32_t>(load_global(plane + offset + 2 * a.I)) << 16;
       staged.rows[k] = value;
     }
   }
@@ -750,12 +754,10 @@ struct ScreenContext {
     for (int bl = 0; bl < blocks; ++bl) {
       const int columns = 4 * sh.union_groups[bl];
       const int8_t *tr = trits(bl);
+      // half 0 starts every chain from an inline zero; half 1 (more than 64
+      // union columns) accumulates
       v4i acc[kTilesPerWave][3];
-#pragma unroll
-      for (int ti = 0; ti < kTilesPerWave; ++ti)
-#pragma unroll
-        for (int d = 0; d < 3; ++d) acc[ti][d] = v4i{0, 0, 0, 0};
-      for (int half = 0; half * kHalfCoords < columns; ++half) {
+      auto contract = [&](int half, bool accumulate) {
         v4i bv[3];
 #pragma unroll
         for (int d = 0; d < 3; ++d)
@@ -763,15 +765,17 @@ struct ScreenContext {
               &sh.digits[bl][(d * kPairTile + pp) * kDigitStride + half * kHalfCoords + k0]);
 #pragma unroll
         for (int ti = 0; ti < kTilesPerWave; ++ti) {
-          const int tile = wave + 4 * ti;
-          if (tile >= kRowTiles) break;
+          const int tile = min(wave + 4 * ti, kRowTiles - 1);
           const v4i av = *reinterpret_cast<const v4i *>(
               &tr[(tile * 16 + pp) * kTritStride + half * kHalfCoords + k0]);
 #pragma unroll
           for (int d = 0; d < 3; ++d)
-            acc[ti][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[d], acc[ti][d], 0, 0, 0);
+            acc[ti][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                av, bv[d], accumulate ? acc[ti][d] : v4i{0, 0, 0, 0}, 0, 0, 0);
         }
-      }
+      };
+      contract(0, false);
+      if (columns > kHalfCoords) contract(1, true);
       if (pp < count) {
         const int shift = sh.pair_shift[bl][pp];
         const float norm2 = sh.pair_norm2[bl][pp];
@@ -798,8 +802,9 @@ struct ScreenContext {
     // store this chunk's split partial projections
     if (pp < count) {
       const int t = sh.pair_token[pp], slot = sh.pair_slot[pp];
-      float *parts = a.parts + (static_cast<long>(t) * a.splits + s) * 2 * a.N + slot * a.I;
-      float *vparts = kGh5 ? a.vparts + (parts - a.parts) : nullptr;
+      // element offsets below 2^31: capacity * K <= 8192, splits <= 8, N <= 16384
+      const uint32_t lane_base =
+          static_cast<uint32_t>((t * a.splits + s) * 2 * a.N + slot * a.I);
 #pragma unroll
       for (int ti = 0; ti < kTilesPerWave; ++ti) {
         if (wave + 4 * ti >= kRowTiles) break;
@@ -809,9 +814,9 @@ struct ScreenContext {
           const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
           const int byte = row / 5, channel = 80 * chunk + 5 * (byte / 2) + row % 5;
           if (byte >= nbytes || channel >= a.I) continue;
-          const int offset = (byte & 1) * a.N + channel;
-          parts[offset] = part[i];
-          if (kGh5) vparts[offset] = vpart[i];
+          const uint32_t offset = lane_base + static_cast<uint32_t>((byte & 1) * a.N + channel);
+          a.parts[offset] = part[i];
+          if (kGh5) a.vparts[offset] = vpart[i];
         }
       }
     }
