@@ -224,74 +224,95 @@ constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column blo
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
 
-__device__ void route_and_group(const PrepareArgs &a) {
-  __shared__ __align__(16) int16_t sorted[kMaxPairs];
-  __shared__ int16_t routed[kMaxPairs];
-  __shared__ int counts[kMaxExperts];
-  __shared__ int segment_count[kPrepareThreads];
-  __shared__ int expert_start[kPrepareThreads], expert_tile[kPrepareThreads];
-  __shared__ int scratch[32];
+struct RouteShared {
+  alignas(16) int16_t sorted[kMaxPairs];
+  int16_t routed[kMaxPairs];
+  int counts[kMaxExperts];
+  int segment_count[kPrepareThreads];
+  int expert_start[kPrepareThreads], expert_tile[kPrepareThreads];
+  int scratch[32];
+};
+
+template <bool kIds64, bool kWeights16>
+__device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShared &shared) {
+  int16_t *sorted = shared.sorted;
+  int16_t *routed = shared.routed;
+  int *counts = shared.counts;
+  int *segment_count = shared.segment_count;
+  int *expert_start = shared.expert_start, *expert_tile = shared.expert_tile;
+  int *scratch = shared.scratch;
   const int tid = threadIdx.x;
   const int T = a.T, K = a.K;
   const int pairs = T * K;
   constexpr int kPerThread = kMaxPairs / kPrepareThreads;
-  // raw ids (outside [0, E) -> -1: no local expert, reads nothing) and each
-  // pair's own router weight, all loads issued together
   auto weight_of = [&](int q) {
-    return (a.flags & CFMOE_WEIGHTS_BF16)
-               ? bf16f(static_cast<const uint16_t *>(a.router_weights)[q])
-               : static_cast<const float *>(a.router_weights)[q];
+    return kWeights16 ? bf16f(load_global(static_cast<const uint16_t *>(a.router_weights) + q))
+                      : load_global(static_cast<const float *>(a.router_weights) + q);
   };
-  // (clamped indices: no branch around the loads, so they issue together)
-  float own_weight[kPerThread];
-  int raw_id[kPerThread];
-  const int rounds = (pairs + kPrepareThreads - 1) / kPrepareThreads;
+  // raw ids (outside [0, E) -> -1: no local expert, reads nothing); the
+  // formats are template arguments, so the loads of a batch of 8 pairs per
+  // thread are issued unconditionally (clamped index) and together
+  constexpr int kBatch = 8;
+  for (int q0 = 0; q0 * kPrepareThreads < pairs; q0 += kBatch) {
+    int raw_id[kBatch];
 #pragma unroll
-  for (int q = 0; q < kPerThread; ++q) {
-    if (q >= rounds) break;
-    const int p = min(tid + kPrepareThreads * q, pairs - 1);
-    raw_id[q] = (a.flags & CFMOE_IDS_INT64)
-                    ? static_cast<int>(load_global(static_cast<const int64_t *>(a.router_ids) + p))
-                    : load_global(static_cast<const int32_t *>(a.router_ids) + p);
-    own_weight[q] =
-        (a.flags & CFMOE_WEIGHTS_BF16)
-            ? bf16f(load_global(static_cast<const uint16_t *>(a.router_weights) + p))
-            : load_global(static_cast<const float *>(a.router_weights) + p);
-  }
+    for (int q = 0; q < kBatch; ++q) {
+      const int p = min(tid + kPrepareThreads * (q0 + q), pairs - 1);
+      if (kIds64) {
+        const int32_t *words = static_cast<const int32_t *>(a.router_ids) + 2 * p;
+        const int low = load_global(words), high = load_global(words + 1);
+        raw_id[q] = high == (low >> 31) ? low : -1;  // outside the int32 range
+      } else {
+        raw_id[q] = load_global(static_cast<const int32_t *>(a.router_ids) + p);
+      }
+    }
 #pragma unroll
-  for (int q = 0; q < kPerThread; ++q) {
-    if (q >= rounds) break;
-    const int p = tid + kPrepareThreads * q;
-    if (p < pairs) routed[p] = static_cast<int16_t>((raw_id[q] < 0 || raw_id[q] >= a.E) ? -1 : raw_id[q]);
+    for (int q = 0; q < kBatch; ++q) {
+      const int p = tid + kPrepareThreads * (q0 + q);
+      if (p < pairs)
+        routed[p] = static_cast<int16_t>((raw_id[q] < 0 || raw_id[q] >= a.E) ? -1 : raw_id[q]);
+    }
   }
   __syncthreads();
   // slot k of a token moves to its rank among the token's ids (ties by slot);
   // its weight is the sum of the weights of equal ids (progressive.py:369-375)
+  for (int q0 = 0; q0 * kPrepareThreads < pairs; q0 += kBatch) {
+    float own_weight[kBatch];
 #pragma unroll
-  for (int q = 0; q < kPerThread; ++q) {
-    const int p = tid + kPrepareThreads * q;
-    if (p >= pairs) continue;
-    const int t = p / K, k = p % K;
-    const bool active = is_active(a.padding, t);
-    const int id = routed[p];
-    int rank = 0, equal = 0;
-    for (int j = 0; j < K; ++j) {
-      const int other = routed[t * K + j];
-      rank += other < id || (other == id && j < k);
-      equal += other == id;
-    }
-    float w = 0.0f;
-    if (active) {
-      if (equal == 1) {
-        w = 0.0f + own_weight[q];
-      } else {
-        for (int j = 0; j < K; ++j)
-          if (routed[t * K + j] == id) w += weight_of(t * K + j);
+    for (int q = 0; q < kBatch; ++q)
+      own_weight[q] = weight_of(min(tid + kPrepareThreads * (q0 + q), pairs - 1));
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) {
+      const int p = tid + kPrepareThreads * (q0 + q);
+      if (p >= pairs) break;
+      const int t = p / K, k = p % K;
+      const bool active = is_active(a.padding, t);
+      const int id = routed[p];
+      int rank = 0, equal = 0;
+      for (int j0 = 0; j0 < K; j0 += 8) {
+        int other[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) other[j] = routed[t * K + min(j0 + j, K - 1)];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (j0 + j >= K) break;
+          rank += other[j] < id || (other[j] == id && j0 + j < k);
+          equal += other[j] == id;
+        }
       }
+      float w = 0.0f;
+      if (active) {
+        if (equal == 1) {
+          w = 0.0f + own_weight[q];
+        } else {
+          for (int j = 0; j < K; ++j)
+            if (routed[t * K + j] == id) w += weight_of(t * K + j);
+        }
+      }
+      a.ids[t * K + rank] = id;
+      a.weights[t * K + rank] = w;
+      sorted[t * K + rank] = static_cast<int16_t>(active ? id : -1);
     }
-    a.ids[t * K + rank] = id;
-    a.weights[t * K + rank] = w;
-    sorted[t * K + rank] = static_cast<int16_t>(active ? id : -1);
   }
   const int padded = (pairs + 7) / 8 * 8;
   for (int p = pairs + tid; p < padded; p += kPrepareThreads) sorted[p] = -1;
@@ -398,8 +419,15 @@ __device__ void route_and_group(const PrepareArgs &a) {
 
 __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
   // block 0 routes and groups (the longest block, dispatched first)
+  __shared__ RouteShared route_shared;
   if (a.route && blockIdx.x == 0) {
-    route_and_group(a);
+    if (a.flags & CFMOE_IDS_INT64) {
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<true, true>(a, route_shared);
+      else route_and_group<true, false>(a, route_shared);
+    } else {
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<false, true>(a, route_shared);
+      else route_and_group<false, false>(a, route_shared);
+    }
     return;
   }
   const int cell_block = static_cast<int>(blockIdx.x) - (a.route ? 1 : 0);
