@@ -148,6 +148,29 @@ __device__ __forceinline__ uint64_t lanes_below(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
 
+// Sum of a wave's 64 values at lane 0 in the xor-butterfly tree (levels m =
+// 1, 2, ..., 32: each level adds the neighbouring block of m lanes). After a
+// level every lane of a block holds the same bits (a + b == b + a exactly),
+// so any lane of the partner block serves: DPP quad permutes for m = 1, 2,
+// the half-row and row mirrors for m = 4, 8, and lane reads of the four row
+// sums for m = 16, 32. No LDS crossbar traffic.
+template <int kControl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kControl, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sum_lane0(float v) {
+  v = dpp_add<0xb1>(v);   // quad_perm [1, 0, 3, 2]: xor 1
+  v = dpp_add<0x4e>(v);   // quad_perm [2, 3, 0, 1]: xor 2
+  v = dpp_add<0x141>(v);  // row_half_mirror: the other 4 lanes of the 8
+  v = dpp_add<0x140>(v);  // row_mirror: the other 8 lanes of the 16
+  const float s0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float s1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float s2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float s3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (s0 + s1) + (s2 + s3);
+}
+
 // ---------------------------------------------------------------------------
 // block-wide reductions (thread order)
 
@@ -1267,11 +1290,8 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
         u = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, u);
       }
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-      g = g + __shfl_xor(g, m);
-      u = u + __shfl_xor(u, m);
-    }
+    g = wave_sum_lane0(g);
+    u = wave_sum_lane0(u);
   }
   if (lane == 0) {
     const long address = static_cast<long>(t) * 2 * a.N + logical;
@@ -1387,11 +1407,8 @@ __global__ __launch_bounds__(256) void group_exact_kernel(GroupExactArgs a) {
         uu = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, uu);
       }
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-      g = g + __shfl_xor(g, m);
-      uu = uu + __shfl_xor(uu, m);
-    }
+    g = wave_sum_lane0(g);
+    uu = wave_sum_lane0(uu);
     if (lane == 0) exact_results(a, t, target, g, uu);
   }
 }
