@@ -375,8 +375,11 @@ def _rocprof_rows(directory: str, suffix: str) -> list[dict]:
 def summarize_trace(directory: str, command: str) -> str:
     """Per-kernel launch statistics of a rocprofv3 --kernel-trace --stats run."""
     durations: dict[str, list[int]] = {}
+    reader_kernels = set(STAGE_KERNELS.values()) | {"select_all_kernel", "group_exact_kernel"}
     for row in _rocprof_rows(directory, "kernel_trace.csv"):
         name = _short_name(row["Kernel_Name"])
+        if name not in reader_kernels:
+            continue  # setup work (weight generation, recovery bank, probe)
         durations.setdefault(name, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
     lines = [f"command: {command}", f"source_sha256_16: {source_digest()}", "",
              f"{'kernel':34s} {'calls':>7s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'total_ms':>10s}"]
