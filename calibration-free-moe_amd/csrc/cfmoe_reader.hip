@@ -545,8 +545,10 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
 //
 // Workgroup = (touched expert z, block split s, group of up to kMaxChunks
 // 32-byte column chunks). A chunk's 32 code bytes per coordinate carry 160
-// trit rows (byte column j holds rows 5 j .. 5 j + 4 of one gate or up
-// channel group). For every block of the split: the expert's pairs' kept
+// trit rows, ordered (plane, channel): rows 0..79 are the chunk's 80 gate
+// channels and rows 80..159 its 80 up channels, so byte column j (plane j % 2,
+// channels 5 (j / 2) .. + 4) fills rows 80 (j % 2) + 5 (j / 2) + d and the four
+// rows an MFMA lane holds are four consecutive channels. For every block of the split: the expert's pairs' kept
 // coordinates and grid values are staged in LDS once, their union is formed,
 // the union's code bytes are decoded to int8 trits ([row][coordinate]) chunk
 // by chunk, and contracted with the pairs' 21-bit grid values split into
@@ -666,9 +668,9 @@ struct ScreenContext {
   ScreenShared &sh;
   int tid, lane, wave, e, B, body, c_begin, c_count, b_begin, blocks, count, s;
   const uint8_t *expert_codes;
-  // per staged word: body-layout code byte offset at chunk 0 (bits 0..23) and
-  // the union coordinate (bits 24..30); -1 when the word is dead
-  int fetch_info[kMaxSpan][kWordsPerThread];
+  // per staged word: its union coordinate, or 0 for a dead word (no
+  // coordinate), which then reads a word of the block that reaches no stored row
+  int fetch_coord[kMaxSpan][kWordsPerThread];
   __device__ int8_t *trits(int bl) const {
     return reinterpret_cast<int8_t *>(sh.arena) + bl * ScreenShared::kTritBytes;
   }
@@ -679,47 +681,41 @@ struct ScreenContext {
     for (int bl = 0; bl < kMaxSpan; ++bl)
 #pragma unroll
       for (int i = 0; i < kWordsPerThread; ++i) {
-        const int item = tid + 256 * i;
-        const int u = item / 8, w = item % 8;
+        const int u = (tid + 256 * i) / 8;
         const bool live = bl < blocks && u < sh.union_count[bl];
-        const int coord = live ? sh.union_list[bl][u] : 0;
-        fetch_info[bl][i] =
-            live ? (((b_begin + bl) * 128 + coord) * body + 4 * w) | (coord << 24) : -1;
+        fetch_coord[bl][i] = live ? sh.union_list[bl][u] : 0;
       }
   }
 
   // Issue the loads of chunk ci: 4 code words per block and the chunk's FP16
-  // scale (and residual) rows. The last chunk of a stride that is not a
-  // multiple of 32 bytes lives in the block-paired 16-byte tail section.
-  // Every load is issued unconditionally (dead ones read the expert's first
-  // word and are replaced), so no branch separates the loads from their uses
-  // and the wait before a chunk covers only that chunk's loads. Plain
+  // scale (and residual) rows. Word w of coordinate c of block b sits at
+  // b 128 body + c body + g0 + 4 w in the body, or, in the last chunk of a
+  // stride that is not a multiple of 32 bytes, at the block-paired 16-byte
+  // tail section: B 128 body + (b / 2) 4096 + (b % 2) 16 + 32 c + 4 w. The
+  // thread's word w = tid % 8 is the same for all its words, so a load is one
+  // multiply-add on the coordinate and a uniform base. Every load is issued
+  // unconditionally and stays inside the expert's codes: a chunk past the
+  // workgroup's range reloads its last chunk, and tail words past the 16
+  // bytes reread word 0 of their row; such values reach no stored row. Plain
   // (L2-allocating) loads: the next chunks of a coordinate share its line.
   __device__ void fetch(int ci, Staged &staged) const {
-    const int chunk = c_begin + ci;
+    const int chunk = c_begin + min(ci, c_count - 1);
     const int g0 = chunk * kChunkBytes;
     const bool tail = g0 >= body;
     const bool chunk_live = ci < c_count;
-    const int tail_words = (a.stride - g0) / 4;
-    // dead words (no chunk, no coordinate, past the tail) read the chunk's
-    // first word: their values reach only zero-digit columns or unused rows
-    const uint8_t *chunk_codes = expert_codes + (tail ? 0 : g0);
+    const int w = tid % 8;
+    const uint32_t row_bytes = tail ? 32u : static_cast<uint32_t>(body);
+    const uint32_t w4 = (tail && 4 * w >= a.stride - g0) ? 0u : static_cast<uint32_t>(4 * w);
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
-      const int b = b_begin + bl;
-      const int tail_base = B * 128 * body + (b / 2) * 128 * 32 + (b % 2) * 16;
+      const int b = b_begin + min(bl, blocks - 1);
+      const long block_base = tail ? static_cast<long>(B) * 128 * body + (b / 2) * 4096 + (b % 2) * 16
+                                   : static_cast<long>(b) * 128 * body + g0;
+      const uint8_t *base = expert_codes + block_base;
 #pragma unroll
-      for (int i = 0; i < kWordsPerThread; ++i) {
-        const int info = fetch_info[bl][i];
-        const int w = (tid + 256 * i) % 8;
-        const bool live = chunk_live && info >= 0 && (!tail || w < tail_words);
-        const uint32_t offset =
-            live ? static_cast<uint32_t>(tail ? tail_base + ((info >> 24) & 127) * 32 + 4 * w
-                                              : (info & 0xffffff))
-                 : 0u;
-        staged.words[bl][i] =
-            load_global(reinterpret_cast<const uint32_t *>(chunk_codes + offset));
-      }
+      for (int i = 0; i < kWordsPerThread; ++i)
+        staged.words[bl][i] = load_global(reinterpret_cast<const uint32_t *>(
+            base + (static_cast<uint32_t>(fetch_coord[bl][i]) * row_bytes + w4)));
     }
     // the chunk's FP16 scale (and residual) rows; dead rows read row 0
     const int nbytes = min(kChunkBytes, a.stride - g0);
@@ -727,10 +723,11 @@ struct ScreenContext {
     for (int k = 0; k < 2; ++k) {
       const int item = tid + 256 * k;
       const int bl = min(item / kChunkRows, kMaxSpan - 1), row = item % kChunkRows;
-      const int j = row / 5, channel = 80 * chunk + 5 * (j / 2) + row % 5;
-      const bool live = chunk_live && item < blocks * kChunkRows && j < nbytes && channel < a.I;
+      const int gate_up = row / 80, cc = row % 80, channel = 80 * chunk + cc;
+      const bool live = chunk_live && item < blocks * kChunkRows &&
+                        2 * (cc / 5) + gate_up < nbytes && channel < a.I;
       const uint16_t *plane = a.stats + (static_cast<long>(e) * B + b_begin + min(bl, blocks - 1)) * 4 * a.I;
-      const uint32_t offset = live ? static_cast<uint32_t>((j % 2) * a.I + channel) : 0u;
+      const uint32_t offset = live ? static_cast<uint32_t>(gate_up * a.I + channel) : 0u;
       uint32_t value = load_global(plane + offset);
       if (kGh5) value |= static_cast<uint32_t>(load_global(plane + offset + 2 * a.I)) << 16;
       staged.rows[k] = value;
@@ -784,10 +781,11 @@ struct ScreenContext {
         for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
           for (int i = 0; i < 4; ++i) code[jj][i] = sh.lut[(word[i] >> (8 * jj)) & 255u];
-        int8_t *out = trits(bl) + 4 * g + 20 * jw * kTritStride;
+        // bytes 4 jw + jj: plane jj % 2, channels 5 (2 jw + jj / 2) .. + 4
+        int8_t *out = trits(bl) + 4 * g + 10 * jw * kTritStride;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          int8_t *row = out + 5 * jj * kTritStride;
+          int8_t *row = out + (80 * (jj & 1) + 5 * (jj >> 1)) * kTritStride;
 #pragma unroll
           for (int d = 0; d < 4; ++d)
             *reinterpret_cast<uint32_t *>(row + d * kTritStride) =
@@ -856,18 +854,21 @@ struct ScreenContext {
       // element offsets below 2^31: capacity * K <= 8192, splits <= 8, N <= 16384
       const uint32_t lane_base =
           static_cast<uint32_t>((t * a.splits + s) * 2 * a.N + slot * a.I);
+      // the lane's four rows of a tile are four consecutive channels of one
+      // plane: one 16-byte store (all four rows are live or none: 80 and the
+      // live row bound 5 nbytes / 2 are multiples of 4, and so is I)
 #pragma unroll
       for (int ti = 0; ti < kTilesPerWave; ++ti) {
         if (wave + 4 * ti >= kRowTiles) break;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = ti * 4 + r;
-          const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
-          const int byte = row / 5, channel = 80 * chunk + 5 * (byte / 2) + row % 5;
-          if (byte >= nbytes || channel >= a.I) continue;
-          const uint32_t offset = lane_base + static_cast<uint32_t>((byte & 1) * a.N + channel);
-          a.parts[offset] = part[i];
-          if (kGh5) a.vparts[offset] = vpart[i];
+        const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16);
+        const int gate_up = row / 80, cc = row % 80, channel = 80 * chunk + cc;
+        if (2 * cc < 5 * nbytes && channel < a.I) {
+          const uint32_t offset = lane_base + static_cast<uint32_t>(gate_up * a.N + channel);
+          *reinterpret_cast<float4 *>(a.parts + offset) =
+              make_float4(part[4 * ti], part[4 * ti + 1], part[4 * ti + 2], part[4 * ti + 3]);
+          if (kGh5)
+            *reinterpret_cast<float4 *>(a.vparts + offset) = make_float4(
+                vpart[4 * ti], vpart[4 * ti + 1], vpart[4 * ti + 2], vpart[4 * ti + 3]);
         }
       }
     }
@@ -1884,6 +1885,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   if (!weights || !workspace || !hidden || !router_ids || !router_weights || !out)
     return fail(CFMOE_EINVAL, "NULL argument");
   if (tokens < 1 || tokens > workspace->capacity) return fail(CFMOE_EINVAL, "tokens out of range");
+  // the screen writes its split partials with 16-byte stores
+  if ((reinterpret_cast<uintptr_t>(workspace->screen_parts) |
+       reinterpret_cast<uintptr_t>(workspace->screen_variance_parts)) % 16)
+    return fail(CFMOE_EINVAL, "screen_parts and screen_variance_parts must be 16-byte aligned");
   const Shape s = shape_of(dims);
   if (tokens * s.K > kMaxPairs) return fail(CFMOE_EINVAL, "tokens * top_k exceeds 8192 pairs");
   if (s.R > 0 && (!weights->encoder_t || !weights->decoder))

@@ -90,7 +90,9 @@ typedef struct cfmoe_weights {
 
 /* Caller-allocated scratch, sized for `capacity` tokens (sizes in bytes from
  * cfmoe_workspace_sizes). Layouts match the reference workspace
- * (progressive.py:2868-3121) where the Python operator exposes them. */
+ * (progressive.py:2868-3121) where the Python operator exposes them. Every
+ * buffer is 16-byte aligned (checked for the screen partials, which take
+ * 16-byte stores). */
 typedef struct cfmoe_workspace {
   int32_t capacity;
   int32_t *ids;               /* [cap, K] sorted local expert ids */
