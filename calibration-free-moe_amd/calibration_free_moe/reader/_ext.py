@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 POINT = 1
 GELU = 2
@@ -55,6 +55,7 @@ class WeightPointers(ctypes.Structure):
         ("decoder", ctypes.c_void_p),
         ("signs", ctypes.c_void_p),
         ("threshold", ctypes.c_void_p),
+        ("trit_planes", ctypes.c_void_p),
     ]
 
 
@@ -66,6 +67,7 @@ WORKSPACE_FIELDS = (
     ("coordinates", "int32"),
     ("qvals", "int32"),
     ("qexp", "int32"),
+    ("qsums", "int32"),
     ("norm2", "float32"),
     ("partial", "float32"),
     ("variances", "float32"),
@@ -133,6 +135,12 @@ def library() -> ctypes.CDLL:
     ]
     lib.cfmoe_launch_stage.restype = ctypes.c_int
     lib.cfmoe_launch_stage.argtypes = [ctypes.c_int32] + lib.cfmoe_forward.argtypes
+    lib.cfmoe_trit_plane_bytes.restype = ctypes.c_int64
+    lib.cfmoe_trit_plane_bytes.argtypes = [ctypes.POINTER(Dims)]
+    lib.cfmoe_pack_trit_planes.restype = ctypes.c_int
+    lib.cfmoe_pack_trit_planes.argtypes = [
+        ctypes.POINTER(Dims), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p
+    ]
     lib.cfmoe_prepare_input.restype = ctypes.c_int
     lib.cfmoe_prepare_input.argtypes = [
         ctypes.POINTER(Dims),
@@ -167,3 +175,10 @@ def workspace_sizes(dims: Dims, capacity: int) -> list[int]:
     if written < 0:
         check(-written)
     return list(sizes)
+
+
+def trit_plane_bytes(dims: Dims) -> int:
+    size = library().cfmoe_trit_plane_bytes(ctypes.byref(dims))
+    if size < 0:
+        check(-size)
+    return size

@@ -177,6 +177,7 @@ class ReaderWorkspace:
         )
         self.sketch_values = buffer("qvals", (capacity, blocks, keep))
         self.sketch_exponents = buffer("qexp", (capacity, blocks))
+        self.sketch_sums = buffer("qsums", (capacity, blocks))
         self.sketch_norms = buffer("norm2", (capacity, blocks))
         self.partial = buffer("partial", (capacity, 2, n))
         self.variances = buffer("variances", (capacity, 2, n))
@@ -235,7 +236,8 @@ class ReaderWorkspace:
         self.screen_dense = torch.empty((0, blocks), dtype=torch.bool, device=device)
         buffers = (
             self.ids, self.weights, self.sketch_planes, self.sketch_coordinates,
-            self.sketch_values, self.sketch_exponents, self.sketch_norms, self.partial,
+            self.sketch_values, self.sketch_exponents, self.sketch_sums, self.sketch_norms,
+            self.partial,
             self.variances, self.screen_parts, self.screen_variance_parts,
             self.activations, self.completed, self.selected, *self.candidate_ids,
             *self.scores, self.starts, self.counts, self.tile_starts,
@@ -264,6 +266,7 @@ _WORKSPACE_ATTRS = (
     ("coordinates", "sketch_coordinates"),
     ("qvals", "sketch_values"),
     ("qexp", "sketch_exponents"),
+    ("qsums", "sketch_sums"),
     ("norm2", "sketch_norms"),
     ("partial", "partial"),
     ("variances", "variances"),
@@ -426,6 +429,23 @@ class ProgressiveReader:
         self.sketch_resident_bytes = (
             self.sketch_codes.numel() + self.sketch_statistics.numel() * 2
         )
+        # The screen reads the codes through a 2-bit repacking in the order of
+        # its matrix-core operands, built once here (64 I H / 128 bytes per
+        # expert); the reference streams the codes themselves.
+        self.sketch_trit_planes = torch.empty(0, dtype=torch.int32, device=device)
+        if plan.final_count < plan.candidate_count:
+            dims = _dims(plan, e, rank)
+            self.sketch_trit_planes = torch.empty(
+                _ext.trit_plane_bytes(dims) // 4, dtype=torch.int32, device=device
+            )
+            _ext.check(
+                _ext.library().cfmoe_pack_trit_planes(
+                    ctypes.byref(dims),
+                    self.sketch_codes.data_ptr(),
+                    self.sketch_trit_planes.data_ptr(),
+                    torch.cuda.current_stream(device).cuda_stream,
+                )
+            )
         self.norms = down.float().square().sum(1).sqrt()
         self.native_gu = gate_up.detach()
         self.down = down.detach()
@@ -530,6 +550,7 @@ class ProgressiveReader:
             _pointer(self.decoder),
             _pointer(self.sketch_signs),
             _pointer(self.selection_threshold),
+            _pointer(self.sketch_trit_planes),
         )
         self._workspace_c = workspace.pointers(self.read_work)
         self._workspace_c.next_ids = _pointer(self.candidate_ids[1])

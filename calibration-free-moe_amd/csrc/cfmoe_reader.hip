@@ -26,6 +26,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
+
 #include "cfmoe_reader.h"
 
 namespace cfmoe {
@@ -144,6 +146,17 @@ __device__ __forceinline__ uint4 load_global(const uint4 *p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint2 load_global(const uint2 *p) {
+  const u32x2 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x2 *>(
+      reinterpret_cast<uintptr_t>(p));
+  return make_uint2(v.x, v.y);
+}
+
+// Load source of dead lanes (no branch around a load, no select after it).
+__device__ const uint4 kZeroVector = {0, 0, 0, 0};
+
 __device__ __forceinline__ uint64_t lanes_below(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
@@ -229,6 +242,7 @@ struct PrepareArgs {
   int32_t *coords;
   int32_t *qvals;
   int32_t *qexp;
+  int32_t *qsums;
   float *norm2;
   int32_t *group_experts;
   int32_t *group_starts;
@@ -243,6 +257,7 @@ struct PrepareArgs {
 };
 
 constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
+constexpr int kWorkspaceBuffers = 29;  // cfmoe_workspace pointers after capacity
 constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
@@ -524,18 +539,25 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
   int exponent = 0;
   if (peak) frexpf(__uint_as_float(peak), &exponent);
   const int shift = peak ? 20 - exponent : 0;
+  const int32_t q0 = kept0 && peak ? static_cast<int32_t>(rintf(ldexpf(v0, shift))) : 0;
+  const int32_t q1 = kept1 && peak ? static_cast<int32_t>(rintf(ldexpf(v1, shift))) : 0;
+  // sum of the cell's grid values (exact in any order: |q| <= 2^20, 128 values)
+  int qsum = q0 + q1;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) qsum += __shfl_xor(qsum, m);
   if (lane == 0) {
     a.norm2[cell] = sq;
     a.qexp[cell] = shift;
+    a.qsums[cell] = qsum;
   }
   if (kept0) {
     a.planes[cell * keep + pos0] = v0;
-    a.qvals[cell * keep + pos0] = peak ? static_cast<int32_t>(rintf(ldexpf(v0, shift))) : 0;
+    a.qvals[cell * keep + pos0] = q0;
     if (keep < 128) a.coords[cell * keep + pos0] = lane;
   }
   if (kept1) {
     a.planes[cell * keep + pos1] = v1;
-    a.qvals[cell * keep + pos1] = peak ? static_cast<int32_t>(rintf(ldexpf(v1, shift))) : 0;
+    a.qvals[cell * keep + pos1] = q1;
     if (keep < 128) a.coords[cell * keep + pos1] = 64 + lane;
   }
 }
@@ -543,53 +565,68 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
 // ---------------------------------------------------------------------------
 // screen (progressive.py:478-1108, expert-major as :2428-2606)
 //
-// Workgroup = (touched expert z, block split s, group of up to kMaxChunks
-// 32-byte column chunks). A chunk's 32 code bytes per coordinate carry 160
-// trit rows, ordered (plane, channel): rows 0..79 are the chunk's 80 gate
-// channels and rows 80..159 its 80 up channels, so byte column j (plane j % 2,
-// channels 5 (j / 2) .. + 4) fills rows 80 (j % 2) + 5 (j / 2) + d and the four
-// rows an MFMA lane holds are four consecutive channels. For every block of the split: the expert's pairs' kept
-// coordinates and grid values are staged in LDS once, their union is formed,
-// the union's code bytes are decoded to int8 trits ([row][coordinate]) chunk
-// by chunk, and contracted with the pairs' 21-bit grid values split into
-// three int8 digits by v_mfma_i32_16x16x64_i8. Integer sums are exact, so each
-// (row, pair) gets the dot any other order would give; the block's grid
-// exponent and FP16 scale then feed the split's FMA chain in block order.
+// Trit planes. The sketch codes hold five trits per byte (byte = sum of
+// (t_d + 1) 3^d; byte column j of a coordinate row is plane j % 2, channels
+// 5 (j / 2) .. + 4; sketch.py:84-150). The reader repacks them once per layer
+// (pack_trit_planes_kernel) into 2-bit digits t + 1 laid out as the screen's
+// MFMA A operands: for expert e, block b, row tile rt (gate/up rows
+// 16 rt .. 16 rt + 15, rows 0..I-1 gate channels, I..2I-1 up channels) and
+// lane l, the uint2 at ((e B + b) RT + rt) 64 + l (RT = 2I / 16) holds in its
+// word h the 16 digits of row 16 rt + l % 16 at coordinates
+// 64 h + 16 (l / 16) + k, k = 0..15, digit k at bits 8 (k % 4) + 2 (k / 4).
+// (word >> 2 s) & 0x03030303 is then operand dword s (k = 4 s .. 4 s + 3):
+// one 8-byte coalesced load and eight bit operations give a lane both of its
+// operands for a block. 64 I B bytes per expert (2 bits per trit).
 
-struct GroupScreenArgs {
-  const uint8_t *codes;
-  const uint16_t *stats;
-  const int32_t *coords;
-  const int32_t *qvals;
-  const int32_t *qexp;
-  const float *norm2;
-  const int32_t *group_experts;
-  const int32_t *group_starts;
-  const int32_t *group_counts;
-  const int32_t *group_pairs;
-  const int32_t *group_total;
-  float *parts;
-  float *vparts;
-  long storage;
-  int H, I, K, N, keep, stride, splits, span, chunks, gh5;
-};
-
-constexpr int kChunkBytes = 32;
-constexpr int kChunkRows = 5 * kChunkBytes;  // 160
-constexpr int kRowTiles = kChunkRows / 16;   // 10
+constexpr int kRowTile = 16;
 constexpr int kPairTile = 16;
 static_assert(kPairTile == kGroupPairs, "a screen workgroup holds one grouping tile");
-constexpr int kCoordStride = 128;            // union slots per block
-// LDS row strides, padded so that the lanes of a wave spread over the banks
-constexpr int kDigitStride = 144;            // bytes per pair row of a digit plane
-constexpr int kTritStride = 144;             // bytes per trit row (128 union columns)
-constexpr int kRawStride = 9;                // words per staged coordinate (8 + 1)
-constexpr int kTilesPerWave = (kRowTiles + 3) / 4;
-constexpr int kMaxChunks = 4;
-constexpr int kMaxSpan = 2;  // rotation blocks per split (H <= 2048)
-constexpr int kHalfCoords = 64;  // union columns per MFMA pass (K = 64)
+constexpr int kMaxSpan = 2;        // rotation blocks per split (H <= 2048)
+constexpr int kDigitStride = 144;  // bytes per pair row of a digit plane (128 + pad)
+constexpr int kMaxRows = 2048;     // 2 I gate/up rows of one expert (I <= 1024)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct PackArgs {
+  const uint8_t *codes;
+  uint2 *planes;
+  long storage;  // code bytes per expert
+  long total;    // uint2 words: E B RT 64
+  int I, B, body;
+};
+
+__global__ __launch_bounds__(256) void pack_trit_planes_kernel(PackArgs a) {
+  const long index = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (index >= a.total) return;
+  const int lane = static_cast<int>(index % 64);
+  const int RT = 2 * a.I / kRowTile;
+  const long tile = index / 64;
+  const int rt = static_cast<int>(tile % RT);
+  const int b = static_cast<int>((tile / RT) % a.B);
+  const long e = tile / RT / a.B;
+  const int row = kRowTile * rt + lane % 16;
+  const int gate_up = row / a.I, channel = row % a.I;
+  const int j = 2 * (channel / 5) + gate_up, d = channel % 5;
+  const uint32_t power = d == 0 ? 1u : d == 1 ? 3u : d == 2 ? 9u : d == 3 ? 27u : 81u;
+  const uint8_t *codes = a.codes + e * a.storage;
+  // body: [block][coordinate][body bytes]; the last 16 bytes of a stride that
+  // is not a multiple of 32 sit in block-paired tail rows [block / 2][coordinate][32]
+  const long column = j < a.body
+                          ? static_cast<long>(b) * 128 * a.body + j
+                          : static_cast<long>(a.B) * 128 * a.body + (b / 2) * 4096 + (b % 2) * 16 +
+                                (j - a.body);
+  const int coordinate_bytes = j < a.body ? a.body : 32;
+  uint32_t word[2] = {0u, 0u};
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int c = 64 * h + 16 * (lane / 16) + k;
+      const uint32_t digit = (codes[column + static_cast<long>(c) * coordinate_bytes] / power) % 3u;
+      word[h] |= digit << (8 * (k % 4) + 2 * (k / 4));
+    }
+  a.planes[index] = make_uint2(word[0], word[1]);
+}
 
 __device__ __forceinline__ void grid_digits(int q, int &d0, int &d1, int &d2) {
   d0 = ((q + 128) & 255) - 128;
@@ -598,417 +635,215 @@ __device__ __forceinline__ void grid_digits(int q, int &d0, int &d1, int &d2) {
   d2 = (rest - d1) >> 8;
 }
 
-// Chunk pipeline of the screen: codes of chunk ci + kRing are in flight (in
-// registers) while chunk ci is decoded and contracted.
-constexpr int kRing = 2;
-constexpr int kWordsPerThread = kCoordStride * (kChunkBytes / 4) / 256;  // 4
-constexpr int kMaxRows = 2048;  // 2 I rows of one expert (I <= 1024)
+__device__ __forceinline__ v4i expand_digits(uint32_t x) {
+  return v4i{static_cast<int>(x & 0x03030303u), static_cast<int>((x >> 2) & 0x03030303u),
+             static_cast<int>((x >> 4) & 0x03030303u), static_cast<int>((x >> 6) & 0x03030303u)};
+}
+
+__device__ __forceinline__ float half_at(uint32_t word, int high) {
+  return static_cast<float>(
+      __builtin_bit_cast(_Float16, static_cast<uint16_t>(high ? word >> 16 : word & 0xffffu)));
+}
+
+// Screen workgroup = (tile z, block split s, range of row tiles). The tile's
+// pairs' kept grid values are staged once as three int8 digit planes
+// ([block][digit][pair][coordinate], zero at coordinates a pair did not keep)
+// and held in registers as MFMA B operands; each wave then walks its row tiles
+// with no barrier: load the row tile's planes and FP16 scales (one tile ahead),
+// expand the digits t + 1, and contract with v_mfma_i32_16x16x64_i8 (16 rows x
+// 16 pairs x 64 coordinates, two halves, one MFMA per grid digit). The digit-0
+// chain starts from -sum(q), so acc0 + acc1 256 + acc2 65536 is the exact
+// integer sum of t q over the kept coordinates; the block's grid exponent and
+// FP16 scale then feed the split's FMA chain in block order
+// (progressive.py:1111-1160).
+
+struct GroupScreenArgs {
+  const uint2 *planes;
+  const uint16_t *stats;
+  const int32_t *coords;
+  const int32_t *qvals;
+  const int32_t *qexp;
+  const int32_t *qsums;
+  const float *norm2;
+  const int32_t *group_experts;
+  const int32_t *group_starts;
+  const int32_t *group_counts;
+  const int32_t *group_pairs;
+  const int32_t *group_total;
+  float *parts;
+  float *vparts;
+  int H, I, K, N, keep, splits, span, parts_per_segment, tiles_per_part;
+};
 
 struct ScreenShared {
-  // One arena serves both phases. Phase 1 stages the pairs' kept coordinates
-  // and packed grid digits; phase 2 holds the trit tiles of one chunk for
-  // every block of the split: [block][160 rows][128 union columns].
-  static constexpr int kStageCoordBytes = kMaxSpan * kPairTile * 128;
-  static constexpr int kStageBytes = kStageCoordBytes + kMaxSpan * kPairTile * 128 * 4;
-  static constexpr int kTritBytes = kChunkRows * kTritStride;
-  static constexpr int kPhase2Bytes = kMaxSpan * kTritBytes;
-  static constexpr int kArenaBytes = kStageBytes > kPhase2Bytes ? kStageBytes : kPhase2Bytes;
-  alignas(16) uint8_t arena[kArenaBytes];
-  // The chunk's code words of every block: [block][union slot][8 words + 1].
-  alignas(16) uint32_t raw[kMaxSpan][kCoordStride * kRawStride];
-  // Digit planes of the split's blocks: [block][digit][pair][union column].
-  alignas(16) int8_t digits[kMaxSpan][3 * kPairTile * kDigitStride];
-  // FP16 scale and residual of the chunk's 160 rows for each block.
-  uint16_t scale[kMaxSpan][kChunkRows];
-  uint16_t residual[kMaxSpan][kChunkRows];
-  // code byte -> its 5 trits as int8: (t0..t3) in x, t4 in y
-  uint2 lut[256];
-  uint32_t mask[kMaxSpan][4];
-  uint8_t union_list[kMaxSpan][128];
-  int union_count[kMaxSpan];
-  int union_groups[kMaxSpan];
+  alignas(16) int8_t digits[kMaxSpan][3][kPairTile][kDigitStride];
   int pair_token[kPairTile], pair_slot[kPairTile];
-  int pair_shift[kMaxSpan][kPairTile];
-  float pair_norm2[kMaxSpan][kPairTile];
+  int qsum[kMaxSpan][kPairTile];
+  int shift[kMaxSpan][kPairTile];
+  float norm2[kMaxSpan][kPairTile];
 };
 
-// Union slot u of a block with G = ceil(U / 4) slot groups sits in MFMA
-// column 4 (u % G) + u / G: the four slots of a column group are G apart, so
-// the lanes decoding consecutive groups read raw rows 9 words apart (no bank
-// conflicts), and the columns in use stay within ceil(U / 4) * 4.
-__device__ __forceinline__ int union_column(int u, int groups) {
-  return 4 * (u % groups) + u / groups;
-}
-
-// Byte d of each of four words, packed into one word (v_perm_b32).
-__device__ __forceinline__ uint32_t gather_byte(uint32_t w0, uint32_t w1, uint32_t w2,
-                                                uint32_t w3, int d) {
-  const uint32_t select = static_cast<uint32_t>(d) | (static_cast<uint32_t>(4 + d) << 8) |
-                          0x0c0c0000u;
-  const uint32_t low = __builtin_amdgcn_perm(w1, w0, select);
-  const uint32_t high = __builtin_amdgcn_perm(w3, w2, select);
-  return __builtin_amdgcn_perm(high, low, 0x05040100u);
-}
-
-// Load sources of dead lanes (no branch around a load, no select after it).
-__device__ const uint32_t kZeroCodeWord = 0x79797979u;  // four zero-trit bytes
-__device__ const uint16_t kZeroHalves[2] = {0, 0};
-__device__ const uint4 kZeroVector = {0, 0, 0, 0};
-
-// One chunk's loads in flight: code words of every block and the chunk's
-// FP16 scale | residual << 16 rows (2 per thread).
-struct Staged {
-  uint32_t words[kMaxSpan][kWordsPerThread];
-  uint32_t rows[2];
+// One row tile's loads: both blocks' operand words and FP16 scale (and
+// residual) words of the lane's four rows.
+struct RowTileLoads {
+  uint2 words[kMaxSpan];
+  uint2 scale[kMaxSpan];
+  uint2 residual[kMaxSpan];
 };
 
 template <bool kGh5>
-struct ScreenContext {
-  const GroupScreenArgs &a;
-  ScreenShared &sh;
-  int tid, lane, wave, e, B, body, c_begin, c_count, b_begin, blocks, count, s;
-  const uint8_t *expert_codes;
-  // per staged word: its union coordinate, or 0 for a dead word (no
-  // coordinate), which then reads a word of the block that reaches no stored row
-  int fetch_coord[kMaxSpan][kWordsPerThread];
-  __device__ int8_t *trits(int bl) const {
-    return reinterpret_cast<int8_t *>(sh.arena) + bl * ScreenShared::kTritBytes;
-  }
-
-  // Offsets of the union coordinates' code words of this pair tile.
-  __device__ void setup_fetch() {
-#pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl)
-#pragma unroll
-      for (int i = 0; i < kWordsPerThread; ++i) {
-        const int u = (tid + 256 * i) / 8;
-        const bool live = bl < blocks && u < sh.union_count[bl];
-        fetch_coord[bl][i] = live ? sh.union_list[bl][u] : 0;
-      }
-  }
-
-  // Issue the loads of chunk ci: 4 code words per block and the chunk's FP16
-  // scale (and residual) rows. Word w of coordinate c of block b sits at
-  // b 128 body + c body + g0 + 4 w in the body, or, in the last chunk of a
-  // stride that is not a multiple of 32 bytes, at the block-paired 16-byte
-  // tail section: B 128 body + (b / 2) 4096 + (b % 2) 16 + 32 c + 4 w. The
-  // thread's word w = tid % 8 is the same for all its words, so a load is one
-  // multiply-add on the coordinate and a uniform base. Every load is issued
-  // unconditionally and stays inside the expert's codes: a chunk past the
-  // workgroup's range reloads its last chunk, and tail words past the 16
-  // bytes reread word 0 of their row; such values reach no stored row. Plain
-  // (L2-allocating) loads: the next chunks of a coordinate share its line.
-  __device__ void fetch(int ci, Staged &staged) const {
-    const int chunk = c_begin + min(ci, c_count - 1);
-    const int g0 = chunk * kChunkBytes;
-    const bool tail = g0 >= body;
-    const bool chunk_live = ci < c_count;
-    const int w = tid % 8;
-    const uint32_t row_bytes = tail ? 32u : static_cast<uint32_t>(body);
-    const uint32_t w4 = (tail && 4 * w >= a.stride - g0) ? 0u : static_cast<uint32_t>(4 * w);
-#pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl) {
-      const int b = b_begin + min(bl, blocks - 1);
-      const long block_base = tail ? static_cast<long>(B) * 128 * body + (b / 2) * 4096 + (b % 2) * 16
-                                   : static_cast<long>(b) * 128 * body + g0;
-      const uint8_t *base = expert_codes + block_base;
-#pragma unroll
-      for (int i = 0; i < kWordsPerThread; ++i)
-        staged.words[bl][i] = load_global(reinterpret_cast<const uint32_t *>(
-            base + (static_cast<uint32_t>(fetch_coord[bl][i]) * row_bytes + w4)));
-    }
-    // the chunk's FP16 scale (and residual) rows; dead rows read row 0
-    const int nbytes = min(kChunkBytes, a.stride - g0);
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int item = tid + 256 * k;
-      const int bl = min(item / kChunkRows, kMaxSpan - 1), row = item % kChunkRows;
-      const int gate_up = row / 80, cc = row % 80, channel = 80 * chunk + cc;
-      const bool live = chunk_live && item < blocks * kChunkRows &&
-                        2 * (cc / 5) + gate_up < nbytes && channel < a.I;
-      const uint16_t *plane = a.stats + (static_cast<long>(e) * B + b_begin + min(bl, blocks - 1)) * 4 * a.I;
-      const uint32_t offset = live ? static_cast<uint32_t>(gate_up * a.I + channel) : 0u;
-      uint32_t value = load_global(plane + offset);
-      if (kGh5) value |= static_cast<uint32_t>(load_global(plane + offset + 2 * a.I)) << 16;
-      staged.rows[k] = value;
-    }
-  }
-
-  // Decode, contract and chain chunk ci whose code words are in `staged`.
-  // Three barriers per chunk: (A) the previous chunk's trit tiles and chunk
-  // rows are consumed; (B) this chunk's code words and rows are in LDS;
-  // (C) its trit tiles are complete.
-  __device__ void process(int ci, const Staged &staged) const {
-    const int chunk = c_begin + ci;
-    const int g0 = chunk * kChunkBytes;
-    const int nbytes = min(kChunkBytes, a.stride - g0);
-    __syncthreads();  // (A)
-#pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl)
-#pragma unroll
-      for (int i = 0; i < kWordsPerThread; ++i) {
-        const int item = tid + 256 * i;
-        sh.raw[bl][(item / 8) * kRawStride + item % 8] = staged.words[bl][i];
-      }
-    // the chunk's FP16 scale (and residual) rows of every block
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int item = tid + 256 * k;
-      if (item < kMaxSpan * kChunkRows) {
-        sh.scale[item / kChunkRows][item % kChunkRows] = static_cast<uint16_t>(staged.rows[k]);
-        if (kGh5)
-          sh.residual[item / kChunkRows][item % kChunkRows] =
-              static_cast<uint16_t>(staged.rows[k] >> 16);
-      }
-    }
-    __syncthreads();  // (B)
-    // decode: item = (slot group g, code word jw) -> 4 byte columns x 5 digits.
-    // Branch-free so that all LDS reads issue together: items past the union
-    // (g >= G), past the chunk's bytes or of an absent second block write
-    // trit rows or columns that no MFMA output uses (zero digits or rows that
-    // are never stored); every index stays inside the tiles.
-    {
-      const int g = tid % 32, jw = tid / 32;
-#pragma unroll
-      for (int bl = 0; bl < kMaxSpan; ++bl) {
-        const int G = max(sh.union_groups[bl], 1);
-        uint32_t word[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          word[i] = sh.raw[bl][min(g + G * i, kCoordStride - 1) * kRawStride + jw];
-        uint2 code[4][4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) code[jj][i] = sh.lut[(word[i] >> (8 * jj)) & 255u];
-        // bytes 4 jw + jj: plane jj % 2, channels 5 (2 jw + jj / 2) .. + 4
-        int8_t *out = trits(bl) + 4 * g + 10 * jw * kTritStride;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          int8_t *row = out + (80 * (jj & 1) + 5 * (jj >> 1)) * kTritStride;
-#pragma unroll
-          for (int d = 0; d < 4; ++d)
-            *reinterpret_cast<uint32_t *>(row + d * kTritStride) =
-                gather_byte(code[jj][0].x, code[jj][1].x, code[jj][2].x, code[jj][3].x, d);
-          *reinterpret_cast<uint32_t *>(row + 4 * kTritStride) =
-              gather_byte(code[jj][0].y, code[jj][1].y, code[jj][2].y, code[jj][3].y, 0);
-        }
-      }
-    }
-    __syncthreads();  // (C)
-    float part[kTilesPerWave * 4], vpart[kTilesPerWave * 4];
-#pragma unroll
-    for (int i = 0; i < kTilesPerWave * 4; ++i) part[i] = vpart[i] = 0.0f;
-    const int pp = lane % 16, k0 = 16 * (lane / 16);
-    for (int bl = 0; bl < blocks; ++bl) {
-      const int columns = 4 * sh.union_groups[bl];
-      const int8_t *tr = trits(bl);
-      // half 0 starts every chain from an inline zero; half 1 (more than 64
-      // union columns) accumulates
-      v4i acc[kTilesPerWave][3];
-      auto contract = [&](int half, bool accumulate) {
-        v4i bv[3];
-#pragma unroll
-        for (int d = 0; d < 3; ++d)
-          bv[d] = *reinterpret_cast<const v4i *>(
-              &sh.digits[bl][(d * kPairTile + pp) * kDigitStride + half * kHalfCoords + k0]);
-#pragma unroll
-        for (int ti = 0; ti < kTilesPerWave; ++ti) {
-          const int tile = min(wave + 4 * ti, kRowTiles - 1);
-          const v4i av = *reinterpret_cast<const v4i *>(
-              &tr[(tile * 16 + pp) * kTritStride + half * kHalfCoords + k0]);
-#pragma unroll
-          for (int d = 0; d < 3; ++d)
-            acc[ti][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
-                av, bv[d], accumulate ? acc[ti][d] : v4i{0, 0, 0, 0}, 0, 0, 0);
-        }
-      };
-      contract(0, false);
-      if (columns > kHalfCoords) contract(1, true);
-      if (pp < count) {
-        const int shift = sh.pair_shift[bl][pp];
-        const float norm2 = sh.pair_norm2[bl][pp];
-#pragma unroll
-        for (int ti = 0; ti < kTilesPerWave; ++ti) {
-          if (wave + 4 * ti >= kRowTiles) break;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int i = ti * 4 + r;
-            const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16) + r;
-            const int sum = acc[ti][0][r] + (acc[ti][1][r] << 8) + (acc[ti][2][r] << 16);
-            const float dot = ldexpf(static_cast<float>(sum), -shift);
-            const float sc = static_cast<float>(__builtin_bit_cast(_Float16, sh.scale[bl][row]));
-            part[i] = fmaf(dot, sc, part[i]);
-            if (kGh5) {
-              const float rs =
-                  static_cast<float>(__builtin_bit_cast(_Float16, sh.residual[bl][row]));
-              vpart[i] = fmaf(rs, norm2, vpart[i]);
-            }
-          }
-        }
-      }
-    }
-    // store this chunk's split partial projections
-    if (pp < count) {
-      const int t = sh.pair_token[pp], slot = sh.pair_slot[pp];
-      // element offsets below 2^31: capacity * K <= 8192, splits <= 8, N <= 16384
-      const uint32_t lane_base =
-          static_cast<uint32_t>((t * a.splits + s) * 2 * a.N + slot * a.I);
-      // the lane's four rows of a tile are four consecutive channels of one
-      // plane: one 16-byte store (all four rows are live or none: 80 and the
-      // live row bound 5 nbytes / 2 are multiples of 4, and so is I)
-#pragma unroll
-      for (int ti = 0; ti < kTilesPerWave; ++ti) {
-        if (wave + 4 * ti >= kRowTiles) break;
-        const int row = (wave + 4 * ti) * 16 + 4 * (lane / 16);
-        const int gate_up = row / 80, cc = row % 80, channel = 80 * chunk + cc;
-        if (2 * cc < 5 * nbytes && channel < a.I) {
-          const uint32_t offset = lane_base + static_cast<uint32_t>(gate_up * a.N + channel);
-          *reinterpret_cast<float4 *>(a.parts + offset) =
-              make_float4(part[4 * ti], part[4 * ti + 1], part[4 * ti + 2], part[4 * ti + 3]);
-          if (kGh5)
-            *reinterpret_cast<float4 *>(a.vparts + offset) = make_float4(
-                vpart[4 * ti], vpart[4 * ti + 1], vpart[4 * ti + 2], vpart[4 * ti + 3]);
-        }
-      }
-    }
-  }
-};
-
-// Stage a tile's pairs for the split's blocks: kept coordinates, their union
-// per block and the grid digits in union-column order.
-template <bool kGh5>
-__device__ void stage_tile(const GroupScreenArgs &a, ScreenShared &sh, int z, int b_begin,
-                           int blocks, int &count) {
-  const int tid = threadIdx.x;
+__global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
+  __shared__ ScreenShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int segment = blockIdx.x / a.parts_per_segment;
+  const int part = blockIdx.x % a.parts_per_segment;
+  const int z = segment / a.splits, s = segment % a.splits;
+  if (z >= *a.group_total) return;
   const int B = a.H / 128;
-  const int keep = a.keep;
+  const int RT = 2 * a.I / kRowTile;
+  const int rt_begin = part * a.tiles_per_part;
+  const int rt_end = min(RT, rt_begin + a.tiles_per_part);
+  if (rt_begin >= rt_end) return;
+  const int e = a.group_experts[z];
   const int first_pair = a.group_starts[z];
-  count = a.group_counts[z];
-  uint8_t(*staged_coords)[kPairTile][128] =
-      reinterpret_cast<uint8_t(*)[kPairTile][128]>(sh.arena);
-  uint32_t(*staged_digits)[kPairTile][128] = reinterpret_cast<uint32_t(*)[kPairTile][128]>(
-      sh.arena + ScreenShared::kStageCoordBytes);
-  __syncthreads();  // the previous segment's tiles and digits are consumed
+  const int count = a.group_counts[z];
+  const int b_begin = s * a.span, blocks = min(B, b_begin + a.span) - b_begin;
+  const int keep = a.keep;
+
+  // ---- stage the tile's digits, grid exponents and sums
+  for (int i = tid; i < static_cast<int>(sizeof(sh.digits) / 16); i += 256)
+    reinterpret_cast<uint4 *>(&sh.digits[0][0][0][0])[i] = make_uint4(0u, 0u, 0u, 0u);
   if (tid < count) {
     const int pair = a.group_pairs[first_pair + tid];
     sh.pair_token[tid] = pair / a.K;
     sh.pair_slot[tid] = pair % a.K;
   }
-  if (tid < kMaxSpan * 4) sh.mask[tid / 4][tid % 4] = 0;
   __syncthreads();
-  for (int item = tid; item < blocks * count * keep; item += 256) {
-    const int bl = item / (count * keep), rest = item % (count * keep);
-    const int pp = rest / keep, j = rest % keep;
-    const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
-    const int coord = keep < 128 ? a.coords[cell * keep + j] : j;
-    int d0, d1, d2;
-    grid_digits(a.qvals[cell * keep + j], d0, d1, d2);
-    staged_coords[bl][pp][j] = static_cast<uint8_t>(coord);
-    staged_digits[bl][pp][j] = (static_cast<uint32_t>(d0) & 255u) |
-                               ((static_cast<uint32_t>(d1) & 255u) << 8) |
-                               ((static_cast<uint32_t>(d2) & 255u) << 16);
-    atomicOr(&sh.mask[bl][coord >> 5], 1u << (coord & 31));
+  if (tid < kMaxSpan * kPairTile) {
+    const int bl = tid / kPairTile, pp = tid % kPairTile;
+    const bool live = bl < blocks && pp < count;
+    const long cell = live ? static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl : 0;
+    sh.qsum[bl][pp] = live ? a.qsums[cell] : 0;
+    sh.shift[bl][pp] = live ? a.qexp[cell] : 0;
+    sh.norm2[bl][pp] = live && kGh5 ? a.norm2[cell] : 0.0f;
   }
-  if (tid < blocks * count) {
-    const int bl = tid / count, pp = tid % count;
-    const long cell = static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl;
-    sh.pair_shift[bl][pp] = a.qexp[cell];
-    sh.pair_norm2[bl][pp] = kGh5 ? a.norm2[cell] : 0.0f;
-  }
-  for (int i = tid; i < kMaxSpan * 3 * kPairTile * kDigitStride / 16; i += 256)
-    reinterpret_cast<uint4 *>(&sh.digits[0][0])[i] = make_uint4(0, 0, 0, 0);
-  __syncthreads();
-  // union lists (ascending coordinates)
-  for (int item = tid; item < blocks * 128; item += 256) {
-    const int bl = item / 128, c = item % 128;
-    const int word = c >> 5, bit = c & 31;
-    int before = 0;
-    for (int w = 0; w < word; ++w) before += __popc(sh.mask[bl][w]);
-    before += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
-    if ((sh.mask[bl][word] >> bit) & 1u) sh.union_list[bl][before] = static_cast<uint8_t>(c);
-    if (c == 127) {
-      const int union_count = before + ((sh.mask[bl][word] >> bit) & 1u);
-      sh.union_count[bl] = union_count;
-      sh.union_groups[bl] = (union_count + 3) / 4;
-    }
-  }
-  if (blocks < kMaxSpan && tid == 0) {
-    sh.union_count[kMaxSpan - 1] = 0;
-    sh.union_groups[kMaxSpan - 1] = 0;
-  }
-  __syncthreads();
-  for (int item = tid; item < blocks * count * keep; item += 256) {
-    const int bl = item / (count * keep), rest = item % (count * keep);
-    const int pp = rest / keep, j = rest % keep;
-    const int coord = staged_coords[bl][pp][j];
-    const int word = coord >> 5, bit = coord & 31;
-    int u = 0;
-    for (int w = 0; w < word; ++w) u += __popc(sh.mask[bl][w]);
-    u += __popc(sh.mask[bl][word] & ((1u << bit) - 1u));
-    const uint32_t packed = staged_digits[bl][pp][j];
-    const int column = union_column(u, sh.union_groups[bl]);
-    sh.digits[bl][(0 * kPairTile + pp) * kDigitStride + column] =
-        static_cast<int8_t>(packed & 255u);
-    sh.digits[bl][(1 * kPairTile + pp) * kDigitStride + column] =
-        static_cast<int8_t>((packed >> 8) & 255u);
-    sh.digits[bl][(2 * kPairTile + pp) * kDigitStride + column] =
-        static_cast<int8_t>((packed >> 16) & 255u);
-  }
-  __syncthreads();
-}
-
-// Fixed grid of resident workgroups. The live work is the flattened list of
-// (tile, split, chunk) items, tile-major, whose length is known only on the
-// device (tile count from the grouping); workgroup w takes the contiguous
-// range [w N / grid, (w + 1) N / grid), so every workgroup gets the same
-// number of chunks to within one and restages its tile only where the range
-// crosses a (tile, split) boundary.
-template <bool kGh5>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void group_screen_kernel(
-    GroupScreenArgs a) {
-  __shared__ ScreenShared sh;
-  const int tid = threadIdx.x;
-  const long items = static_cast<long>(*a.group_total) * a.splits * a.chunks;
-  const long lo = items * blockIdx.x / gridDim.x;
-  const long hi = items * (blockIdx.x + 1) / gridDim.x;
-  if (lo >= hi) return;
   {
-    int value = tid;
-    uint32_t t_lo = 0, t_hi = 0;
-    for (int d = 0; d < 5; ++d) {
-      const uint32_t t8 = static_cast<uint8_t>(static_cast<int8_t>(value % 3 - 1));
-      if (d < 4) t_lo |= t8 << (8 * d); else t_hi = t8;
-      value /= 3;
+    // thread (block bl, kept position j) over the tile's pairs; all loads of
+    // a group of four pairs are issued before any is used
+    const int bl = tid >> 7, j = tid & 127;
+    const bool lane_live = bl < blocks && j < keep;
+    const int jj = min(j, keep - 1);
+    const int block = b_begin + min(bl, blocks - 1);
+#pragma unroll
+    for (int group = 0; group < kPairTile / 4; ++group) {
+      if (4 * group >= count) break;
+      int coord[4], q[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pp = min(4 * group + r, count - 1);
+        const long base = (static_cast<long>(sh.pair_token[pp]) * B + block) * keep + jj;
+        coord[r] = keep < 128 ? a.coords[base] : jj;
+        q[r] = a.qvals[base];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pp = 4 * group + r;
+        if (lane_live && pp < count) {
+          int d0, d1, d2;
+          grid_digits(q[r], d0, d1, d2);
+          sh.digits[bl][0][pp][coord[r]] = static_cast<int8_t>(d0);
+          sh.digits[bl][1][pp][coord[r]] = static_cast<int8_t>(d1);
+          sh.digits[bl][2][pp][coord[r]] = static_cast<int8_t>(d2);
+        }
+      }
     }
-    sh.lut[tid] = make_uint2(t_lo, t_hi);
   }
-  const int B = a.H / 128;
-  for (long index = lo; index < hi;) {
-    const long segment = index / a.chunks;  // (tile, split)
-    const int c_begin = static_cast<int>(index % a.chunks);
-    const int c_count = static_cast<int>(min(static_cast<long>(a.chunks - c_begin), hi - index));
-    index += c_count;
-    const int z = static_cast<int>(segment / a.splits);
-    const int s = static_cast<int>(segment % a.splits);
-    const int e = a.group_experts[z];
-    const int b_begin = s * a.span, blocks = min(B, (s + 1) * a.span) - b_begin;
-    int count;
-    stage_tile<kGh5>(a, sh, z, b_begin, blocks, count);
-    ScreenContext<kGh5> ctx{a, sh, tid, tid & 63, tid >> 6, e, B, a.stride - a.stride % 32,
-                            c_begin, c_count, b_begin, blocks, count, s,
-                            a.codes + static_cast<long>(e) * a.storage, {}};
-    ctx.setup_fetch();
-    Staged ring0, ring1;
-    ctx.fetch(0, ring0);
-    ctx.fetch(1, ring1);
-    for (int ci = 0; ci < c_count; ci += kRing) {
-      ctx.process(ci, ring0);
-      ctx.fetch(ci + kRing, ring0);
-      if (ci + 1 >= c_count) break;
-      ctx.process(ci + 1, ring1);
-      ctx.fetch(ci + 1 + kRing, ring1);
+  __syncthreads();
+
+  // ---- B operands and per-pair constants of this lane's pair column
+  const int pp = lane % 16, k0 = 16 * (lane / 16);
+  v4i operand[kMaxSpan][2][3];
+  v4i start[kMaxSpan];
+  int shift[kMaxSpan];
+  float norm2[kMaxSpan];
+#pragma unroll
+  for (int bl = 0; bl < kMaxSpan; ++bl) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+        operand[bl][h][d] = *reinterpret_cast<const v4i *>(&sh.digits[bl][d][pp][64 * h + k0]);
+    const int qsum = sh.qsum[bl][pp];
+    start[bl] = v4i{-qsum, -qsum, -qsum, -qsum};
+    shift[bl] = sh.shift[bl][pp];
+    norm2[bl] = sh.norm2[bl][pp];
+  }
+  const bool store_lane = pp < count;
+  const int token = sh.pair_token[min(pp, count - 1)], slot = sh.pair_slot[min(pp, count - 1)];
+  // element offsets below 2^31: capacity * K <= 8192, splits <= 8, N <= 16384
+  const uint32_t lane_base = static_cast<uint32_t>((token * a.splits + s) * 2 * a.N + slot * a.I);
+  const int row_in_tile = 4 * (lane / 16);
+  const uint2 *planes = a.planes + (static_cast<long>(e) * B + b_begin) * RT * 64 + lane;
+  const uint16_t *stats = a.stats + (static_cast<long>(e) * B + b_begin) * 4 * a.I + row_in_tile;
+  const int second = blocks > 1 ? 1 : 0;  // block offset of the second load (repeats a lone block)
+
+  auto load = [=](int rt) {
+    RowTileLoads t;
+#pragma unroll
+    for (int bl = 0; bl < kMaxSpan; ++bl) {
+      const int block = bl ? second : 0;
+      t.words[bl] = load_global(planes + (block * RT + rt) * 64);
+      t.scale[bl] = load_global(reinterpret_cast<const uint2 *>(
+          stats + block * 4 * a.I + kRowTile * rt));
+      if (kGh5)
+        t.residual[bl] = load_global(reinterpret_cast<const uint2 *>(
+            stats + block * 4 * a.I + 2 * a.I + kRowTile * rt));
     }
+    return t;
+  };
+
+  int rt = rt_begin + wave;
+  if (rt >= rt_end) return;
+  RowTileLoads current = load(rt);
+  for (; rt < rt_end; rt += 4) {
+    const RowTileLoads next = load(min(rt + 4, rt_end - 1));
+    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f}, vpart[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int bl = 0; bl < kMaxSpan; ++bl) {
+      if (bl >= blocks) break;
+      const v4i a0 = expand_digits(current.words[bl].x);
+      const v4i a1 = expand_digits(current.words[bl].y);
+      v4i acc[3];
+      acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][0], start[bl], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][1], v4i{0, 0, 0, 0}, 0,
+                                                     0, 0);
+      acc[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][2], v4i{0, 0, 0, 0}, 0,
+                                                     0, 0);
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+        acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, operand[bl][1][d], acc[d], 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int sum = acc[0][r] + (acc[1][r] << 8) + (acc[2][r] << 16);
+        const float dot = ldexpf(static_cast<float>(sum), -shift[bl]);
+        const uint32_t sw = r < 2 ? current.scale[bl].x : current.scale[bl].y;
+        part[r] = fmaf(dot, half_at(sw, r & 1), part[r]);
+        if (kGh5) {
+          const uint32_t rw = r < 2 ? current.residual[bl].x : current.residual[bl].y;
+          vpart[r] = fmaf(half_at(rw, r & 1), norm2[bl], vpart[r]);
+        }
+      }
+    }
+    if (store_lane) {
+      const int row = kRowTile * rt + row_in_tile;
+      const int gate_up = row >= a.I ? 1 : 0, channel = row - gate_up * a.I;
+      const uint32_t offset = lane_base + static_cast<uint32_t>(gate_up * a.N + channel);
+      *reinterpret_cast<float4 *>(a.parts + offset) = make_float4(part[0], part[1], part[2], part[3]);
+      if (kGh5)
+        *reinterpret_cast<float4 *>(a.vparts + offset) =
+            make_float4(vpart[0], vpart[1], vpart[2], vpart[3]);
+    }
+    current = next;
   }
 }
 
@@ -1685,19 +1520,18 @@ long tile_bound(int tokens, int top_k, int experts) {
   return pairs < bound ? pairs : bound;
 }
 
-// Screen workgroups per launch: two resident per CU (LDS and VGPR budget),
-// from the current device's CU count (cached per device).
-long screen_workgroups() {
+// Compute units of the current device (cached per device).
+long compute_units() {
   static int cached[64] = {};
   int device = 0;
-  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 512;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
   if (cached[device] == 0) {
     int units = 0;
     if (hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device) !=
             hipSuccess ||
         units <= 0)
       units = 256;
-    cached[device] = 2 * units;
+    cached[device] = units;
   }
   return cached[device];
 }
@@ -1785,6 +1619,7 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.coords = ws->coordinates;
   a.qvals = ws->qvals;
   a.qexp = ws->qexp;
+  a.qsums = ws->qsums;
   a.norm2 = ws->norm2;
   a.group_experts = ws->group_experts;
   a.group_starts = ws->group_starts;
@@ -1826,13 +1661,14 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
   const Shape s = shape_of(dims);
   const int64_t cap = capacity;
   const int64_t n = s.N;
-  const int64_t table[28] = {
+  const int64_t table[kWorkspaceBuffers] = {
       cap * s.K * 4,                          // ids
       cap * s.K * 4,                          // weights
       cap * s.B * s.keep * 4,                 // planes
       cap * s.B * s.keep * 4,                 // coordinates
       cap * s.B * s.keep * 4,                 // qvals
       cap * s.B * 4,                          // qexp
+      cap * s.B * 4,                          // qsums
       cap * s.B * 4,                          // norm2
       cap * 2 * n * 4,                        // partial
       cap * 2 * n * 4,                        // variances
@@ -1856,9 +1692,35 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
       cap * s.K * 4,                          // group_pairs
       4,                                      // group_total
   };
-  const int written = count < 28 ? count : 28;
+  const int written = count < kWorkspaceBuffers ? count : kWorkspaceBuffers;
   for (int i = 0; i < written; ++i) sizes[i] = table[i];
   return written;
+}
+
+int64_t cfmoe_trit_plane_bytes(const cfmoe_dims *dims) {
+  if (int rc = validate(dims)) return -rc;
+  return static_cast<int64_t>(dims->experts) * (dims->hidden / 128) * dims->width * 64;
+}
+
+int cfmoe_pack_trit_planes(const cfmoe_dims *dims, const uint8_t *codes, uint32_t *planes,
+                           cfmoe_stream stream) {
+  if (int rc = validate(dims)) return rc;
+  if (!codes || !planes) return fail(CFMOE_EINVAL, "NULL argument");
+  if (reinterpret_cast<uintptr_t>(planes) % 8)
+    return fail(CFMOE_EINVAL, "trit_planes must be 8-byte aligned");
+  PackArgs a;
+  a.codes = codes;
+  a.planes = reinterpret_cast<uint2 *>(planes);
+  a.I = dims->width;
+  a.B = dims->hidden / 128;
+  a.storage = storage_bytes(2 * a.I, dims->hidden);
+  const int stride = code_stride(2 * a.I);
+  a.body = stride - stride % 32;
+  a.total = static_cast<long>(dims->experts) * a.B * (2 * a.I / kRowTile) * 64;
+  const long blocks = (a.total + 255) / 256;
+  hipLaunchKernelGGL(pack_trit_planes_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("pack_trit_planes");
 }
 
 int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,
@@ -1895,6 +1757,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     return fail(CFMOE_EINVAL, "rank > 0 needs encoder and decoder");
   if ((dims->flags & CFMOE_THRESHOLD) && !weights->threshold)
     return fail(CFMOE_EINVAL, "threshold flag without threshold");
+  if (s.screened && (!weights->trit_planes || reinterpret_cast<uintptr_t>(weights->trit_planes) % 8))
+    return fail(CFMOE_EINVAL, "trit_planes must be an 8-byte aligned cfmoe_pack_trit_planes output");
+  if (s.screened && (!weights->statistics || reinterpret_cast<uintptr_t>(weights->statistics) % 8))
+    return fail(CFMOE_EINVAL, "statistics must be 8-byte aligned (the screen loads four at a time)");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
   const uint32_t flags = dims->flags;
   const bool gh5 = !(flags & CFMOE_POINT);
@@ -1925,11 +1791,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
 
   if (s.screened) {
     GroupScreenArgs sc;
-    sc.codes = weights->codes;
+    sc.planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
     sc.stats = static_cast<const uint16_t *>(weights->statistics);
     sc.coords = workspace->coordinates;
     sc.qvals = workspace->qvals;
     sc.qexp = workspace->qexp;
+    sc.qsums = workspace->qsums;
     sc.norm2 = workspace->norm2;
     sc.group_experts = workspace->group_experts;
     sc.group_starts = workspace->group_starts;
@@ -1938,18 +1805,24 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     sc.group_total = workspace->group_total;
     sc.parts = workspace->screen_parts;
     sc.vparts = workspace->screen_variance_parts;
-    sc.storage = storage_bytes(2 * s.I, s.H);
     sc.H = s.H;
     sc.I = s.I;
     sc.K = s.K;
     sc.N = s.N;
     sc.keep = s.keep;
-    sc.stride = code_stride(2 * s.I);
     sc.splits = s.splits;
     sc.span = s.span;
-    sc.chunks = (sc.stride + kChunkBytes - 1) / kChunkBytes;
-    sc.gh5 = gh5;
-    const long items = screen_workgroups();
+    // (tile, split) segments, each cut into parts of row tiles so that about
+    // four workgroups per CU are live; a part keeps at least one row tile per
+    // wave. Workgroups of tiles past the device's tile count exit at once.
+    const long segments = tile_bound(tokens, s.K, dims->experts) * s.splits;
+    const int row_tiles = 2 * s.I / kRowTile;
+    const long target = 4L * compute_units();
+    long parts = (target + segments - 1) / segments;
+    parts = std::max(1L, std::min(parts, static_cast<long>((row_tiles + 3) / 4)));
+    sc.tiles_per_part = static_cast<int>((row_tiles + parts - 1) / parts);
+    sc.parts_per_segment = (row_tiles + sc.tiles_per_part - 1) / sc.tiles_per_part;
+    const long items = segments * sc.parts_per_segment;
     if (stages & (1u << CFMOE_STAGE_SCREEN)) {
       if (gh5)
         hipLaunchKernelGGL(group_screen_kernel<true>, dim3(static_cast<unsigned>(items)),

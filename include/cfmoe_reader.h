@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 2
+#define CFMOE_ABI_VERSION 3
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -78,7 +78,7 @@ typedef struct cfmoe_dims {
 typedef struct cfmoe_weights {
   const void *gate_up;     /* bf16 [E, 2I, H] */
   const void *down;        /* bf16, physical [E, I, H] (channel-major) */
-  const uint8_t *codes;    /* [E, sketch_storage_bytes(2I, H)] */
+  const uint8_t *codes;    /* [E, sketch_storage_bytes(2I, H)]; read by cfmoe_pack_trit_planes only */
   const void *statistics;  /* fp16, physical [E, H/128, 2, 2I] */
   const float *norms;      /* [E, I] down-column L2 norms */
   const float *geometry;   /* [E, I, 2] (alpha, beta) or NULL */
@@ -86,6 +86,7 @@ typedef struct cfmoe_weights {
   const void *decoder;     /* bf16 [H, R] or NULL */
   const int8_t *signs;     /* [H] rotation signs */
   const float *threshold;  /* [1] selection threshold or NULL */
+  const uint32_t *trit_planes; /* screen layout of `codes` (cfmoe_pack_trit_planes) */
 } cfmoe_weights;
 
 /* Caller-allocated scratch, sized for `capacity` tokens (sizes in bytes from
@@ -101,6 +102,7 @@ typedef struct cfmoe_workspace {
   int32_t *coordinates;       /* [cap, B, keep] their coordinates */
   int32_t *qvals;             /* [cap, B, keep] values on the 21-bit grid */
   int32_t *qexp;              /* [cap, B] grid exponents */
+  int32_t *qsums;             /* [cap, B] sums of the kept grid values */
   float *norm2;               /* [cap, B] squared norm of kept values */
   float *partial;             /* [cap, 2, N] gate/up projections */
   float *variances;           /* [cap, 2, N] */
@@ -127,7 +129,7 @@ typedef struct cfmoe_workspace {
 } cfmoe_workspace;
 
 /* Byte sizes of every workspace buffer, in struct order after `capacity`
- * (28 entries, read_work excluded). Returns the number written. */
+ * (29 entries, read_work excluded). Returns the number written. */
 CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
                           int32_t count);
 
@@ -151,6 +153,20 @@ CFMOE_API int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cf
                        const void *router_ids, const void *router_weights,
                        const uint8_t *padding, void *out, int32_t tokens,
                        const double *charges, cfmoe_stream stream);
+
+/* Bytes of the screen's trit planes for all `experts` (64 * width * hidden /
+ * 128 per expert), or minus an error code. */
+CFMOE_API int64_t cfmoe_trit_plane_bytes(const cfmoe_dims *dims);
+
+/* Repack the sketch codes (the reference's five-trits-per-byte layout,
+ * sketch.py:84-150, validated at progressive.py:3318-3328) into the screen's
+ * resident 2-bit layout `trit_planes` (cfmoe_trit_plane_bytes bytes, 8-byte
+ * aligned): digit t + 1 of every gate/up row and rotated coordinate, in the
+ * order the screen's matrix-core operands are loaded. Run once per layer when
+ * the reader is built (the reference reads the codes directly); no
+ * counterpart call in the reference. */
+CFMOE_API int cfmoe_pack_trit_planes(const cfmoe_dims *dims, const uint8_t *codes,
+                                     uint32_t *trit_planes, cfmoe_stream stream);
 
 /* Routing-independent input rotation ahead of the router
  * (progressive.py:3829-3873). A following cfmoe_forward with

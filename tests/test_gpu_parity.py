@@ -79,6 +79,7 @@ def assert_parity(reader, out, expected, tokens, screened=True):
         got["planes"] = reader.sketch_planes[:t].cpu().numpy()
         got["qvals"] = reader.sketch_values[:t].cpu().numpy()
         got["qexp"] = reader.sketch_exponents[:t].cpu().numpy()
+        got["qsums"] = reader.workspace.sketch_sums[:t].cpu().numpy()
         got["scores"] = reader.scores[0][:t].cpu().numpy()
         if reader.plan.screen_coordinates < 128:
             got["coordinates"] = reader.sketch_coordinates[:t].cpu().numpy()
@@ -88,6 +89,9 @@ def assert_parity(reader, out, expected, tokens, screened=True):
     done = expected["completed"].astype(bool)
     got["activations"] = np.where(done, got["activations"], 0)
     expected = dict(expected, activations=np.where(done, expected["activations"], 0))
+    if screened:
+        # the screen's per-cell sums of the kept grid values
+        expected["qsums"] = expected["qvals"].astype(np.int64).sum(-1).astype(np.int32)
     for name, value in got.items():
         want = expected[name]
         if not np.array_equal(value, want):
