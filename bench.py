@@ -135,6 +135,16 @@ STAGE_BYTES = {"screen": ("sketch",), "exact": ("gate_up",), "down": ("down",),
 STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "group_screen_kernel",
                  "score": "score_kernel", "select": "select_kernel", "exact": "exact_kernel",
                  "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
+GROUP_EXACT_TOKENS = 16  # batches from which the exact stage runs group_exact_kernel
+
+
+def stage_kernel(stage: str, tokens: int) -> str:
+    """Name of the kernel a stage launches at this batch size."""
+    if stage == "exact" and tokens >= GROUP_EXACT_TOKENS:
+        return "group_exact_kernel"
+    return STAGE_KERNELS[stage]
+
+
 SOURCE = os.path.join(ROOT, "calibration-free-moe_amd", "csrc", "cfmoe_reader.hip")
 PROFILES = os.path.join(ROOT, "profiles")
 PROBE_ELEMENTS = 1 << 27  # float32: 512 MiB read + 512 MiB written per probe launch
@@ -480,7 +490,7 @@ def main() -> int:
     probe = stream_probe(device)
     baseline = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     h, i, e, k, layers, tokens, retention, keep, description = CONFIGS[args.config]
-    kernel = STAGE_KERNELS[headline["dominant"]]
+    kernel = stage_kernel(headline["dominant"], headline["tokens"])
     traffic = measured_traffic(kernel, args.config, headline["tokens"], headline["layers"])
     line = {
         "metric": METRIC,

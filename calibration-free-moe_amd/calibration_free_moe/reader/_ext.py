@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 POINT = 1
 GELU = 2
@@ -90,6 +90,8 @@ WORKSPACE_FIELDS = (
     ("group_counts", "int32"),
     ("group_pairs", "int32"),
     ("group_total", "int32"),
+    ("pair_tiles", "int32"),
+    ("tile_masks", "int32"),
 )
 
 

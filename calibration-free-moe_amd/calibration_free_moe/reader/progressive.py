@@ -210,8 +210,10 @@ class ReaderWorkspace:
         self.group_experts = buffer("group_experts", (capacity * k,))
         self.group_starts = buffer("group_starts", (capacity * k,))
         self.group_counts = buffer("group_counts", (capacity * k,))
-        self.group_pairs = buffer("group_pairs", (capacity * k,))
+        self.group_pairs = buffer("group_pairs", (capacity * k * GROUP_ROWS,))
         self.group_total = buffer("group_total", (1,))
+        self.pair_tiles = buffer("pair_tiles", (capacity * k,))
+        self.tile_masks = buffer("tile_masks", (capacity * n,))
         # The reference's last-arrival counters; these kernels need none but the
         # attributes stay (all zero) for callers that inspect them.
         self.screen_counters = torch.zeros(
@@ -243,7 +245,7 @@ class ReaderWorkspace:
             *self.scores, self.starts, self.counts, self.tile_starts,
             self.down_tile_starts, self.down_parts, self.encoder_parts, self.latent,
             self.group_experts, self.group_starts, self.group_counts, self.group_pairs,
-            self.group_total,
+            self.group_total, self.pair_tiles, self.tile_masks,
         )
         self.bytes = sum(t.numel() * t.element_size() for t in buffers)
         self.charged = False
@@ -287,6 +289,8 @@ _WORKSPACE_ATTRS = (
     ("group_counts", "group_counts"),
     ("group_pairs", "group_pairs"),
     ("group_total", "group_total"),
+    ("pair_tiles", "pair_tiles"),
+    ("tile_masks", "tile_masks"),
 )
 
 

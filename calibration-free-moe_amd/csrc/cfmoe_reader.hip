@@ -249,6 +249,7 @@ struct PrepareArgs {
   int32_t *group_counts;
   int32_t *group_pairs;
   int32_t *group_total;
+  int32_t *pair_tiles;
   double *read_work;
   double charges[18];
   int T, H, K, E, keep;
@@ -257,7 +258,7 @@ struct PrepareArgs {
 };
 
 constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
-constexpr int kWorkspaceBuffers = 29;  // cfmoe_workspace pointers after capacity
+constexpr int kWorkspaceBuffers = 31;  // cfmoe_workspace pointers after capacity
 constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
@@ -267,7 +268,7 @@ struct RouteShared {
   int16_t routed[kMaxPairs];
   int counts[kMaxExperts];
   int segment_count[kPrepareThreads];
-  int expert_start[kPrepareThreads], expert_tile[kPrepareThreads];
+  int expert_tile[kPrepareThreads];
   int scratch[32];
 };
 
@@ -277,7 +278,7 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShare
   int16_t *routed = shared.routed;
   int *counts = shared.counts;
   int *segment_count = shared.segment_count;
-  int *expert_start = shared.expert_start, *expert_tile = shared.expert_tile;
+  int *expert_tile = shared.expert_tile;
   int *scratch = shared.scratch;
   const int tid = threadIdx.x;
   const int T = a.T, K = a.K;
@@ -307,8 +308,10 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShare
 #pragma unroll
     for (int q = 0; q < kBatch; ++q) {
       const int p = tid + kPrepareThreads * (q0 + q);
-      if (p < pairs)
+      if (p < pairs) {
         routed[p] = static_cast<int16_t>((raw_id[q] < 0 || raw_id[q] >= a.E) ? -1 : raw_id[q]);
+        a.pair_tiles[p] = -1;  // pairs in no tile (padded token, no local expert)
+      }
     }
   }
   __syncthreads();
@@ -369,23 +372,31 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShare
     }
     return count;
   };
-  // place expert e's pairs among [begin, end) in order from group_pairs[at]
+  // place expert e's pairs among [begin, end) in order from tile slot `at`:
+  // tile z holds its pairs at group_pairs[16 z ..], and pair_tiles maps each
+  // placed pair back to its slot
   auto place = [&](int e, int begin, int end, int at) {
     for (int p = begin; p < end; p += 8) {
       const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
       const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (static_cast<int16_t>(w[i] & 0xffffu) == e) a.group_pairs[at++] = p + 2 * i;
-        if (static_cast<int16_t>(w[i] >> 16) == e) a.group_pairs[at++] = p + 2 * i + 1;
+        if (static_cast<int16_t>(w[i] & 0xffffu) == e) {
+          a.group_pairs[at] = p + 2 * i;
+          a.pair_tiles[p + 2 * i] = at++;
+        }
+        if (static_cast<int16_t>(w[i] >> 16) == e) {
+          a.group_pairs[at] = p + 2 * i + 1;
+          a.pair_tiles[p + 2 * i + 1] = at++;
+        }
       }
     }
   };
   // tiles of at most kGroupPairs pairs, one screen workgroup each
-  auto emit_tiles = [&](int e, int count, int start, int z) {
+  auto emit_tiles = [&](int e, int count, int z) {
     for (int first_pair = 0; first_pair < count; first_pair += kGroupPairs) {
       a.group_experts[z] = e;
-      a.group_starts[z] = start + first_pair;
+      a.group_starts[z] = kGroupPairs * z;
       a.group_counts[z] = min(kGroupPairs, count - first_pair);
       ++z;
     }
@@ -412,36 +423,27 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShare
     const bool leader = e < a.E && part == 0;
     int z = block_exclusive(leader ? (count + kGroupPairs - 1) / kGroupPairs : 0, scratch,
                             &total_tiles);
-    int total_members;
-    const int start = block_exclusive(leader ? count : 0, scratch, &total_members);
-    if (leader) {
-      expert_start[e] = start;
-      expert_tile[e] = z;
-    }
+    if (leader) expert_tile[e] = z;
     __syncthreads();
-    if (e < a.E && mine > 0) place(e, begin, end, expert_start[e] + before);
-    if (leader && count > 0) emit_tiles(e, count, start, z);
+    if (e < a.E && mine > 0) place(e, begin, end, kGroupPairs * expert_tile[e] + before);
+    if (leader && count > 0) emit_tiles(e, count, z);
   } else {
     // each thread owns the contiguous experts [first, last)
     const int span = (a.E + kPrepareThreads - 1) / kPrepareThreads;
     const int first = min(a.E, tid * span), last = min(a.E, first + span);
-    int tiles = 0, members = 0;
+    int tiles = 0;
     for (int e = first; e < last; ++e) {
       const int count = matches(e, 0, padded);
       counts[e] = count;
       tiles += (count + kGroupPairs - 1) / kGroupPairs;
-      members += count;
     }
     int z = block_exclusive(tiles, scratch, &total_tiles);
-    int total_members;
-    int start = block_exclusive(members, scratch, &total_members);
     for (int e = first; e < last; ++e) {
       const int count = counts[e];
       if (count == 0) continue;
-      place(e, 0, padded, start);
-      emit_tiles(e, count, start, z);
+      place(e, 0, padded, kGroupPairs * z);
+      emit_tiles(e, count, z);
       z += (count + kGroupPairs - 1) / kGroupPairs;
-      start += count;
     }
   }
   if (tid == 0) *a.group_total = total_tiles;
@@ -863,6 +865,8 @@ struct ScoreArgs {
   float *scores;
   uint8_t *completed;
   uint8_t *selected;
+  uint32_t *tile_masks;  // cleared here for the select kernel's channel masks (or NULL)
+  long mask_words;
   int I, K, N, splits;
   int gh5, gelu, point;
 };
@@ -871,6 +875,9 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreArgs a) {
   const int logical = blockIdx.x * 256 + threadIdx.x;
   const int t = blockIdx.y;
   if (logical >= a.N) return;
+  // tokens * N >= tiles * I: every mask word has a thread
+  if (a.tile_masks && static_cast<long>(t) * a.N + logical < a.mask_words)
+    a.tile_masks[static_cast<long>(t) * a.N + logical] = 0u;
   const int k = logical / a.I, c = logical % a.I;
   const long stride = 2l * a.N;
   const long base = static_cast<long>(t) * a.splits * stride + logical;
@@ -922,6 +929,8 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreArgs a) {
 struct SelectArgs {
   const float *scores;
   const float *threshold;
+  const int32_t *pair_tiles;  // tile slot 16 z + p of each pair, -1 if none
+  uint32_t *tile_masks;       // [tile][channel] bit p: tile pair p kept it (or NULL)
   int32_t *next_ids;
   uint8_t *selected;
   int32_t *counts;
@@ -939,9 +948,11 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int histogram[2048];
   __shared__ int scratch[32];
   __shared__ int slot_counts[64];
+  __shared__ int slot_tiles[64];
   __shared__ uint32_t shared_bin;
   __shared__ int shared_above;
   const int t = blockIdx.x, tid = threadIdx.x;
+  if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
   // keys: every load issued unconditionally (absent keys read a zero)
@@ -1038,7 +1049,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
     a.selected[static_cast<long>(t) * a.N + i] = keep[j];
     if (keep[j] && position < a.F) {
       a.next_ids[static_cast<long>(t) * a.F + position++] = i;
-      atomicAdd(&slot_counts[i / a.I], 1);
+      const int k = i / a.I;
+      atomicAdd(&slot_counts[k], 1);
+      // the channel's bit for this pair in its tile's mask (OR: any order)
+      const int slot_tile = a.tile_masks ? slot_tiles[k] : -1;
+      if (slot_tile >= 0)
+        atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - k * a.I)],
+                 1u << (slot_tile % kGroupPairs));
     }
   }
   for (int p = kept_total + tid; p < a.F; p += kSelectThreads)
@@ -1140,10 +1157,11 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
 }
 
 // Grouped exact rows (batches of kGroupExactTokens or more, as
-// progressive.py:2655-2718): wave = (16-pair expert tile, channel). One
-// ballot over the tile's pairs finds those that kept the channel; if any did,
-// the channel's gate and up rows are read once and dotted with each such
-// pair's hidden row in the lane order of exact_kernel (identical results).
+// progressive.py:2655-2718): wave = (16-pair expert tile, channel). The
+// select kernel's tile mask names the tile's pairs that kept the channel; it
+// and the tile's pairs (16 slots per tile) are read together. If any pair
+// kept the channel, its gate and up rows are read once and dotted with each
+// such pair's hidden row in the lane order of exact_kernel (identical results).
 // Workgroups past the tiles (one per token) write the zero results of padded
 // tokens and non-local slots, which the grouping leaves out.
 struct GroupExactArgs {
@@ -1160,10 +1178,12 @@ struct GroupExactArgs {
   const int32_t *group_counts;
   const int32_t *group_pairs;
   const int32_t *group_total;
+  const uint32_t *tile_masks;
   float *partial;
   uint16_t *activations;
   uint8_t *completed;
   int H, I, K, N, F, T, gelu, channel_groups, tile_items;
+  int dense;  // every channel kept by every pair (no tile masks)
 };
 
 constexpr int kMaxHidden = 2048;
@@ -1198,17 +1218,12 @@ __global__ __launch_bounds__(256) void group_exact_kernel(GroupExactArgs a) {
   const int z = blockIdx.x / a.channel_groups;
   const int c = (blockIdx.x % a.channel_groups) * 4 + wave;
   if (z >= *a.group_total || c >= a.I) return;
-  const int e = a.group_experts[z], count = a.group_counts[z], first = a.group_starts[z];
+  const int e = a.group_experts[z], count = a.group_counts[z];
   // lane p < count: pair p of the tile
-  int token = 0, logical = 0;
-  bool kept = false;
-  if (lane < count) {
-    const int pair = a.group_pairs[first + lane];
-    token = pair / a.K;
-    logical = (pair % a.K) * a.I + c;
-    kept = a.selected[static_cast<long>(token) * a.N + logical] != 0;
-  }
-  const uint64_t mask = __ballot(kept);
+  const int pair = a.group_pairs[kGroupPairs * z + min(lane, count - 1)];
+  const int token = pair / a.K, logical = (pair % a.K) * a.I + c;
+  const uint64_t mask =
+      a.dense ? (1ull << count) - 1ull : a.tile_masks[static_cast<long>(z) * a.I + c];
   if (!mask) return;
   const uint16_t *grow = a.gate_up + (static_cast<long>(e) * 2 * a.I + c) * a.H;
   const uint16_t *urow = grow + static_cast<long>(a.I) * a.H;
@@ -1625,6 +1640,7 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.group_starts = ws->group_starts;
   a.group_counts = ws->group_counts;
   a.group_pairs = ws->group_pairs;
+  a.pair_tiles = ws->pair_tiles;
   a.group_total = ws->group_total;
   a.read_work = ws->read_work;
   if (charges && (d->flags & CFMOE_ACCOUNT))
@@ -1689,8 +1705,10 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
       cap * s.K * 4,                          // group_experts
       cap * s.K * 4,                          // group_starts
       cap * s.K * 4,                          // group_counts
-      cap * s.K * 4,                          // group_pairs
+      cap * s.K * kGroupPairs * 4,            // group_pairs (16 slots per tile)
       4,                                      // group_total
+      cap * s.K * 4,                          // pair_tiles
+      cap * n * 4,                            // tile_masks (tiles * I <= cap * N)
   };
   const int written = count < kWorkspaceBuffers ? count : kWorkspaceBuffers;
   for (int i = 0; i < written; ++i) sizes[i] = table[i];
@@ -1788,6 +1806,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   sel.I = s.I;
   sel.K = s.K;
   sel.thresholded = (flags & CFMOE_THRESHOLD) != 0;
+  // per-(tile, channel) pair masks for the grouped exact kernel
+  const bool masked = s.screened && tokens >= kGroupExactTokens;
+  sel.pair_tiles = workspace->pair_tiles;
+  sel.tile_masks = masked ? workspace->tile_masks : nullptr;
 
   if (s.screened) {
     GroupScreenArgs sc;
@@ -1853,6 +1875,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     so.gh5 = gh5;
     so.gelu = gelu;
     so.point = !gh5;
+    so.tile_masks = sel.tile_masks;
+    so.mask_words = tile_bound(tokens, s.K, dims->experts) * s.I;
     if (stages & (1u << CFMOE_STAGE_SCORE)) {
       hipLaunchKernelGGL(score_kernel, dim3((s.N + 255) / 256, tokens), dim3(256), 0, stream,
                          so);
@@ -1899,6 +1923,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       gx.group_counts = workspace->group_counts;
       gx.group_pairs = workspace->group_pairs;
       gx.group_total = workspace->group_total;
+      gx.tile_masks = workspace->tile_masks;
+      gx.dense = s.screened ? 0 : 1;
       gx.partial = workspace->partial;
       gx.activations = ex.activations;
       gx.completed = workspace->completed;

@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 3
+#define CFMOE_ABI_VERSION 4
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -121,15 +121,17 @@ typedef struct cfmoe_workspace {
   float *encoder_parts;       /* [cap, K, ceil(I/64), R] */
   float *latent;              /* [cap, R] */
   int32_t *group_experts;     /* [cap * K] expert of each tile of <= 16 pairs, ascending */
-  int32_t *group_starts;      /* [cap * K] first pair of each tile in group_pairs */
+  int32_t *group_starts;      /* [cap * K] first slot of each tile in group_pairs (16 z) */
   int32_t *group_counts;      /* [cap * K] pairs of each tile (1..16) */
-  int32_t *group_pairs;       /* [cap * K] token * K + slot, grouped by expert */
+  int32_t *group_pairs;       /* [cap * K * 16] token * K + slot; tile z at 16 z .. */
   int32_t *group_total;       /* [1] number of tiles */
+  int32_t *pair_tiles;        /* [cap * K] slot 16 z + p of each pair in group_pairs, or -1 */
+  uint32_t *tile_masks;       /* [cap * N] per (tile, channel): bit p set if pair p kept it */
   double *read_work;          /* [20] read statistics (progressive.py:3507-3515) */
 } cfmoe_workspace;
 
 /* Byte sizes of every workspace buffer, in struct order after `capacity`
- * (29 entries, read_work excluded). Returns the number written. */
+ * (31 entries, read_work excluded). Returns the number written. */
 CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
                           int32_t count);
 

@@ -185,16 +185,26 @@ def test_hot_expert_splits_into_screen_tiles():
     tile_experts = ws.group_experts[:total].cpu().tolist()
     starts = ws.group_starts[:total].cpu().tolist()
     counts = ws.group_counts[:total].cpu().tolist()
-    pairs = ws.group_pairs[: tokens * top_k].cpu().tolist()
+    pairs = ws.group_pairs[: 16 * total].cpu().tolist()
+    pair_tiles = ws.pair_tiles[: tokens * top_k].cpu().tolist()
+    masks = ws.tile_masks[: total * 256].cpu().numpy().view(np.uint32).reshape(total, 256)
     assert all(1 <= c <= 16 for c in counts)
     assert tile_experts == sorted(tile_experts)
     assert tile_experts.count(5) == 3 and [c for e, c in zip(tile_experts, counts) if e == 5] == [16, 16, 8]
+    assert starts == [16 * z for z in range(total)]
     sorted_ids = expected["ids"]
+    selected = expected["selected"].reshape(tokens, top_k, 256).astype(bool)
     seen = []
-    for e, first, count in zip(tile_experts, starts, counts):
+    for z, (e, first, count) in enumerate(zip(tile_experts, starts, counts)):
         members = pairs[first:first + count]
         assert members == sorted(members)
         assert all(sorted_ids[p // top_k, p % top_k] == e for p in members)
+        assert [pair_tiles[p] for p in members] == list(range(first, first + count))
+        # bit p of the (tile, channel) mask: pair p of the tile kept the channel
+        want = np.zeros(256, np.uint32)
+        for position, p in enumerate(members):
+            want |= selected[p // top_k, p % top_k].astype(np.uint32) << np.uint32(position)
+        assert np.array_equal(masks[z], want)
         seen += members
     assert sorted(seen) == list(range(tokens * top_k))
 
