@@ -1198,7 +1198,8 @@ __device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, in
   a.completed[static_cast<long>(t) * a.N + logical] = 1;
 }
 
-__global__ __launch_bounds__(256) void group_exact_kernel(GroupExactArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void group_exact_kernel(
+    GroupExactArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
     // zero results of a padded token or of a slot with no local expert
@@ -1241,6 +1242,12 @@ __global__ __launch_bounds__(256) void group_exact_kernel(GroupExactArgs a) {
     const int target = __shfl(logical, pp);
     const uint16_t *xr = a.x + static_cast<long>(t) * a.H;
     float g = 0.0f, uu = 0.0f;
+    // keep the rows packed across pairs (unpacking them once ahead of the
+    // loop would hold 64 more registers and halve the waves per SIMD)
+#pragma unroll
+    for (int j = 0; j < kParts; ++j)
+      asm volatile("" : "+v"(gw[j].x), "+v"(gw[j].y), "+v"(gw[j].z), "+v"(gw[j].w),
+                   "+v"(uw[j].x), "+v"(uw[j].y), "+v"(uw[j].z), "+v"(uw[j].w));
 #pragma unroll
     for (int j = 0; j < kParts; ++j) {
       const int h = 512 * j + 8 * lane;
