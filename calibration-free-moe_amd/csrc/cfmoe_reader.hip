@@ -1289,8 +1289,6 @@ struct EncodeArgs {
 constexpr int kEncodeStride = 72;  // LDS row stride (bf16) of a staged encoder row
 
 __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
-  __shared__ float value[64];
-  __shared__ int skipped[64];
   __shared__ __align__(16) uint16_t coefficients[64 * kEncodeStride];
   const int tile = blockIdx.x, k = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
   const int c = tile * 64 + lane;
@@ -1329,17 +1327,21 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   } else if (skip && local) {
     for (int q = 0; q < a.R; ++q) staged[q] = row[q];
   }
-  value[lane] = v;
-  skipped[lane] = skip;
+  const uint64_t skipped = __ballot(skip);
   __syncthreads();
-  if (lane >= a.R) return;
+  // lane r < R: chain over the tile's skipped channels in order; a kept
+  // channel leaves the sum untouched (a select, not an added zero), so the
+  // loop has no branch and its LDS reads issue together (lanes >= R compute
+  // on their in-bounds staged columns and store nothing)
   float acc = 0.0f;
+#pragma unroll
   for (int j = 0; j < 64; ++j) {
-    if (!skipped[j]) continue;
+    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
     const float coefficient = local ? bf16f(coefficients[j * kEncodeStride + lane]) : 0.0f;
-    acc = fmaf(value[j], coefficient, acc);
+    const float next = fmaf(value, coefficient, acc);
+    acc = (skipped >> j) & 1ull ? next : acc;
   }
-  a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * a.R + lane] = acc;
+  if (lane < a.R) a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * a.R + lane] = acc;
 }
 
 // ---------------------------------------------------------------------------
