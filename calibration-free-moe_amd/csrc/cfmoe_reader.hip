@@ -187,10 +187,34 @@ __device__ __forceinline__ float wave_sum_lane0(float v) {
 // ---------------------------------------------------------------------------
 // block-wide reductions (thread order)
 
+// Integer wave sum, every lane gets the total (exact in any order).
+__device__ __forceinline__ int wave_sum_all(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, false);   // xor 1
+  v += __builtin_amdgcn_mov_dpp(v, 0x4e, 0xf, 0xf, false);   // xor 2
+  v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xf, 0xf, false);  // row_half_mirror
+  v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xf, 0xf, false);  // row_mirror
+  return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+         (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
+}
+
+// Integer inclusive scan over the wave's lanes: shifts of 1, 2, 4, 8 lanes
+// inside each 16-lane row (DPP row_shr, zero from outside the row), then the
+// totals of the rows below (lane reads of lanes 15, 31, 47).
+__device__ __forceinline__ int wave_inclusive(int v) {
+  const int lane = threadIdx.x & 63;
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15);
+  const int r1 = __builtin_amdgcn_readlane(v, 31);
+  const int r2 = __builtin_amdgcn_readlane(v, 47);
+  return v + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
+}
+
 __device__ int block_sum(int v, int *scratch) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  v = wave_sum_all(v);
   __syncthreads();
   if (lane == 0) scratch[wave] = v;
   __syncthreads();
@@ -202,12 +226,7 @@ __device__ int block_sum(int v, int *scratch) {
 // Exclusive prefix over threads in thread order; *total receives the sum.
 __device__ int block_exclusive(int v, int *scratch, int *total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inclusive = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int n = __shfl_up(inclusive, o);
-    if (lane >= o) inclusive += n;
-  }
+  const int inclusive = wave_inclusive(v);
   __syncthreads();
   if (lane == 63) scratch[wave] = inclusive;
   __syncthreads();
