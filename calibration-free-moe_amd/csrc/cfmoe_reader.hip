@@ -963,15 +963,50 @@ struct SelectArgs {
 constexpr int kSelectThreads = 1024;
 constexpr int kSelectKeys = 16;  // keys per thread: N <= 16384
 
+// Histogram slot of a radix bin: one pad word per 32 bins, so that lanes
+// reading bins 32 apart use different LDS banks.
+__device__ __forceinline__ int select_slot(int bin) { return bin + (bin >> 5); }
+constexpr int kSelectSlots = 2048 + 2048 / 32;
+
+// The bin of a radix pass where the count of keys from the top reaches
+// `want`, found by one wave from the pass's histogram: lane l sums the
+// `per_lane` bins below bins - per_lane l, a wave scan finds the lane where
+// the running count reaches `want`, and its bins are scanned the same way,
+// one per lane. Returns the bin; *above receives the count of keys in higher
+// bins.
+__device__ __forceinline__ int select_find_bin(const int *histogram, int bins, int want,
+                                               int *above) {
+  const int lane = threadIdx.x & 63;
+  const int per_lane = bins / kWave;
+  const int top = bins - lane * per_lane;
+  int mine = 0;
+#pragma unroll 8
+  for (int i = 1; i <= per_lane; ++i) mine += histogram[select_slot(top - i)];
+  const int inclusive = wave_inclusive(mine);
+  // want <= the keys left in the pass, so some lane reaches it
+  const uint64_t reached = __ballot(inclusive >= want);
+  const int owner = reached ? __builtin_ctzll(reached) : kWave - 1;
+  const int before = __builtin_amdgcn_readlane(inclusive - mine, owner);
+  // the owner's bins, highest first, one per lane
+  const int owner_top = bins - owner * per_lane;
+  const int count = lane < per_lane ? histogram[select_slot(owner_top - 1 - lane)] : 0;
+  const int running = before + wave_inclusive(count);
+  const uint64_t hit = __ballot(lane < per_lane && running >= want);
+  const int at = hit ? __builtin_ctzll(hit) : per_lane - 1;
+  *above = __builtin_amdgcn_readlane(running - count, at);
+  return owner_top - 1 - at;
+}
+
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
-  __shared__ int histogram[2048];
+  __shared__ int histogram[3][kSelectSlots];
   __shared__ int scratch[32];
   __shared__ int slot_counts[64];
   __shared__ int slot_tiles[64];
-  __shared__ uint32_t shared_bin;
-  __shared__ int shared_above;
+  __shared__ int shared_bin, shared_above;
   const int t = blockIdx.x, tid = threadIdx.x;
   if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
+  for (int i = tid; i < 3 * kSelectSlots; i += kSelectThreads) (&histogram[0][0])[i] = 0;
+  if (tid < 64) slot_counts[tid] = 0;
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
   // keys: every load issued unconditionally (absent keys read a zero)
@@ -993,88 +1028,79 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
     for (int j = 0; j < kSelectKeys; ++j) passing += valid(j) && key[j] >= bound;
     passing = block_sum(passing, scratch);
     want = min(want, passing);
+  } else {
+    __syncthreads();  // the histograms are zero
   }
+  // three radix passes (11/11/10 bits) find the want-th largest key; in each,
+  // wave 0 reads the bin off the LDS histogram between two barriers
   uint32_t prefix = 0, mask = 0;
   if (want > 0) {
     const int shifts[3] = {21, 10, 0};
     const int widths[3] = {11, 11, 10};
+#pragma unroll
     for (int pass = 0; pass < 3; ++pass) {
       const int shift = shifts[pass];
       const uint32_t bins = 1u << widths[pass];
-      for (int i = tid; i < 2048; i += kSelectThreads) histogram[i] = 0;
-      __syncthreads();
 #pragma unroll
       for (int j = 0; j < kSelectKeys; ++j)
         if (valid(j) && (key[j] & mask) == prefix)
-          atomicAdd(&histogram[(key[j] >> shift) & (bins - 1)], 1);
+          atomicAdd(&histogram[pass][select_slot((key[j] >> shift) & (bins - 1))], 1);
       __syncthreads();
-      // thread i owns bins [bins - (i + 1) * per_thread, bins - i * per_thread),
-      // high first; the block scan finds the bin where the count reaches want
-      const int per_thread = static_cast<int>(bins) / kSelectThreads;
-      const int top = static_cast<int>(bins) - tid * per_thread;
-      int mine = 0;
-      for (int i = 1; i <= per_thread; ++i) mine += histogram[top - i];
-      int counted;
-      const int before = block_exclusive(mine, scratch, &counted);
-      if (before < want && before + mine >= want) {
-        int running = before;
-        for (int i = 1; i <= per_thread; ++i) {
-          const int h = histogram[top - i];
-          if (running + h >= want) {
-            shared_bin = static_cast<uint32_t>(top - i);
-            shared_above = running;
-            break;
-          }
-          running += h;
+      if (tid < kWave) {
+        int above;
+        const int bin = select_find_bin(histogram[pass], static_cast<int>(bins), want, &above);
+        if (tid == 0) {
+          shared_bin = bin;
+          shared_above = above;
         }
       }
       __syncthreads();
-      prefix |= shared_bin << shift;
+      prefix |= static_cast<uint32_t>(shared_bin) << shift;
       mask |= (bins - 1) << shift;
       want -= shared_above;
-      __syncthreads();
     }
   }
-  const bool any = a.F > 0 && (a.thresholded ? (want > 0 || mask != 0) : true);
+  const bool any = a.F > 0 && mask != 0;
   // After the passes `prefix` is the cutoff key and `want` the ties it keeps.
+  // One scan of packed (above, tied) counts gives every thread the kept keys
+  // before it: all keys above the cutoff, ties in ascending candidate order.
   const uint32_t cutoff = prefix;
   const int room = want;
-  int tied = 0;
-#pragma unroll
-  for (int j = 0; j < kSelectKeys; ++j) tied += valid(j) && mask != 0 && key[j] == cutoff;
-  int tie_total;
-  int tie_rank = block_exclusive(tied, scratch, &tie_total);
-  bool keep[kSelectKeys];
-  int kept = 0;
+  int above_here = 0, tied_here = 0;
 #pragma unroll
   for (int j = 0; j < kSelectKeys; ++j) {
-    keep[j] = false;
-    if (!valid(j) || mask == 0 || !any) continue;
-    if (key[j] > cutoff) {
-      keep[j] = true;
-    } else if (key[j] == cutoff) {
-      keep[j] = tie_rank < room;
-      ++tie_rank;
-    }
-    kept += keep[j];
+    above_here += any && valid(j) && key[j] > cutoff;
+    tied_here += any && valid(j) && key[j] == cutoff;
   }
-  if (tid < 64) slot_counts[tid] = 0;
-  int kept_total;
-  int position = block_exclusive(kept, scratch, &kept_total);
+  int packed_total;
+  const int packed = block_exclusive(above_here | (tied_here << 16), scratch, &packed_total);
+  const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
+  int above_before = packed & 0xffff, tied_before = packed >> 16;
 #pragma unroll
   for (int j = 0; j < kSelectKeys; ++j) {
     if (!valid(j)) continue;
     const int i = first + j;
-    a.selected[static_cast<long>(t) * a.N + i] = keep[j];
-    if (keep[j] && position < a.F) {
-      a.next_ids[static_cast<long>(t) * a.F + position++] = i;
-      const int k = i / a.I;
-      atomicAdd(&slot_counts[k], 1);
-      // the channel's bit for this pair in its tile's mask (OR: any order)
-      const int slot_tile = a.tile_masks ? slot_tiles[k] : -1;
-      if (slot_tile >= 0)
-        atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - k * a.I)],
-                 1u << (slot_tile % kGroupPairs));
+    bool keep = false;
+    if (any && key[j] > cutoff) {
+      keep = true;
+    } else if (any && key[j] == cutoff) {
+      keep = tied_before < room;
+      ++tied_before;
+    }
+    a.selected[static_cast<long>(t) * a.N + i] = keep;
+    const int position = above_before + min(tied_before - (keep && key[j] == cutoff ? 1 : 0), room);
+    if (keep) {
+      if (key[j] > cutoff) ++above_before;
+      if (position < a.F) {
+        a.next_ids[static_cast<long>(t) * a.F + position] = i;
+        const int k = i / a.I;
+        atomicAdd(&slot_counts[k], 1);
+        // the channel's bit for this pair in its tile's mask (OR: any order)
+        const int slot_tile = a.tile_masks ? slot_tiles[k] : -1;
+        if (slot_tile >= 0)
+          atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - k * a.I)],
+                   1u << (slot_tile % kGroupPairs));
+      }
     }
   }
   for (int p = kept_total + tid; p < a.F; p += kSelectThreads)
