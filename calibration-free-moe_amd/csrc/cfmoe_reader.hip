@@ -731,6 +731,29 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
   const int b_begin = s * a.span, blocks = min(B, b_begin + a.span) - b_begin;
   const int keep = a.keep;
 
+  // the trit planes and scales depend only on the expert and the split: the
+  // wave's first row tile is loaded while the tile's digits are staged
+  const int row_in_tile = 4 * (lane / 16);
+  const uint2 *planes = a.planes + (static_cast<long>(e) * B + b_begin) * RT * 64 + lane;
+  const uint16_t *stats = a.stats + (static_cast<long>(e) * B + b_begin) * 4 * a.I + row_in_tile;
+  const int second = blocks > 1 ? 1 : 0;  // block offset of the second load (repeats a lone block)
+  auto load = [=](int rt) {
+    RowTileLoads t;
+#pragma unroll
+    for (int bl = 0; bl < kMaxSpan; ++bl) {
+      const int block = bl ? second : 0;
+      t.words[bl] = load_global(planes + (block * RT + rt) * 64);
+      t.scale[bl] = load_global(reinterpret_cast<const uint2 *>(
+          stats + block * 4 * a.I + kRowTile * rt));
+      if (kGh5)
+        t.residual[bl] = load_global(reinterpret_cast<const uint2 *>(
+            stats + block * 4 * a.I + 2 * a.I + kRowTile * rt));
+    }
+    return t;
+  };
+  int rt = rt_begin + wave;
+  RowTileLoads current = load(min(rt, rt_end - 1));
+
   // ---- stage the tile's digits, grid exponents and sums
   for (int i = tid; i < static_cast<int>(sizeof(sh.digits) / 16); i += 256)
     reinterpret_cast<uint4 *>(&sh.digits[0][0][0][0])[i] = make_uint4(0u, 0u, 0u, 0u);
@@ -803,37 +826,14 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
   const int token = sh.pair_token[min(pp, count - 1)], slot = sh.pair_slot[min(pp, count - 1)];
   // element offsets below 2^31: capacity * K <= 8192, splits <= 8, N <= 16384
   const uint32_t lane_base = static_cast<uint32_t>((token * a.splits + s) * 2 * a.N + slot * a.I);
-  const int row_in_tile = 4 * (lane / 16);
-  const uint2 *planes = a.planes + (static_cast<long>(e) * B + b_begin) * RT * 64 + lane;
-  const uint16_t *stats = a.stats + (static_cast<long>(e) * B + b_begin) * 4 * a.I + row_in_tile;
-  const int second = blocks > 1 ? 1 : 0;  // block offset of the second load (repeats a lone block)
-
-  auto load = [=](int rt) {
-    RowTileLoads t;
-#pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl) {
-      const int block = bl ? second : 0;
-      t.words[bl] = load_global(planes + (block * RT + rt) * 64);
-      t.scale[bl] = load_global(reinterpret_cast<const uint2 *>(
-          stats + block * 4 * a.I + kRowTile * rt));
-      if (kGh5)
-        t.residual[bl] = load_global(reinterpret_cast<const uint2 *>(
-            stats + block * 4 * a.I + 2 * a.I + kRowTile * rt));
-    }
-    return t;
-  };
-
-  int rt = rt_begin + wave;
   if (rt >= rt_end) return;
-  RowTileLoads current = load(rt);
-  for (; rt < rt_end; rt += 4) {
-    const RowTileLoads next = load(min(rt + 4, rt_end - 1));
+  auto process = [&](const RowTileLoads &tile, int rt_now) {
     float part[4] = {0.0f, 0.0f, 0.0f, 0.0f}, vpart[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
       if (bl >= blocks) break;
-      const v4i a0 = expand_digits(current.words[bl].x);
-      const v4i a1 = expand_digits(current.words[bl].y);
+      const v4i a0 = expand_digits(tile.words[bl].x);
+      const v4i a1 = expand_digits(tile.words[bl].y);
       v4i acc[3];
       acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][0], start[bl], 0, 0, 0);
       acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][1], v4i{0, 0, 0, 0}, 0,
@@ -847,16 +847,16 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
       for (int r = 0; r < 4; ++r) {
         const int sum = acc[0][r] + (acc[1][r] << 8) + (acc[2][r] << 16);
         const float dot = ldexpf(static_cast<float>(sum), -shift[bl]);
-        const uint32_t sw = r < 2 ? current.scale[bl].x : current.scale[bl].y;
+        const uint32_t sw = r < 2 ? tile.scale[bl].x : tile.scale[bl].y;
         part[r] = fmaf(dot, half_at(sw, r & 1), part[r]);
         if (kGh5) {
-          const uint32_t rw = r < 2 ? current.residual[bl].x : current.residual[bl].y;
+          const uint32_t rw = r < 2 ? tile.residual[bl].x : tile.residual[bl].y;
           vpart[r] = fmaf(half_at(rw, r & 1), norm2[bl], vpart[r]);
         }
       }
     }
     if (store_lane) {
-      const int row = kRowTile * rt + row_in_tile;
+      const int row = kRowTile * rt_now + row_in_tile;
       const int gate_up = row >= a.I ? 1 : 0, channel = row - gate_up * a.I;
       const uint32_t offset = lane_base + static_cast<uint32_t>(gate_up * a.N + channel);
       *reinterpret_cast<float4 *>(a.parts + offset) = make_float4(part[0], part[1], part[2], part[3]);
@@ -864,7 +864,20 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
         *reinterpret_cast<float4 *>(a.vparts + offset) =
             make_float4(vpart[0], vpart[1], vpart[2], vpart[3]);
     }
-    current = next;
+  };
+  // three of the wave's row tiles in flight (a load past the range repeats
+  // its last row tile)
+  RowTileLoads second_tile = load(min(rt + 4, rt_end - 1));
+  RowTileLoads third_tile = load(min(rt + 8, rt_end - 1));
+  for (; rt < rt_end; rt += 12) {
+    process(current, rt);
+    current = load(min(rt + 12, rt_end - 1));
+    if (rt + 4 >= rt_end) break;
+    process(second_tile, rt + 4);
+    second_tile = load(min(rt + 16, rt_end - 1));
+    if (rt + 8 >= rt_end) break;
+    process(third_tile, rt + 8);
+    third_tile = load(min(rt + 20, rt_end - 1));
   }
 }
 
