@@ -282,27 +282,40 @@ constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column blo
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
 
+// LDS of the routing block, carved from the launch's dynamic LDS, which the
+// host sizes for the call's pairs and experts (route_lds_bytes): the pairs'
+// ids in routing order (later the per-expert buckets of pair indices) and
+// sorted per token, then per-expert counters and packed prefixes.
 struct RouteShared {
-  alignas(16) int16_t sorted[kMaxPairs];
-  int16_t routed[kMaxPairs];
-  int counts[kMaxExperts];
-  int segment_count[kPrepareThreads];
-  int expert_tile[kPrepareThreads];
-  int scratch[32];
+  int16_t *sorted, *routed;
+  int *counts, *base;
 };
 
+__host__ __device__ inline long route_pairs_padded(int pairs) { return (pairs + 7) / 8 * 8; }
+
+__host__ __device__ inline long route_lds_bytes(int pairs, int experts) {
+  return 2 * 2 * route_pairs_padded(pairs) + 2 * 4 * (experts + 1);
+}
+
+__device__ inline RouteShared route_layout(char *lds, int pairs, int experts) {
+  RouteShared r;
+  const long padded = route_pairs_padded(pairs);
+  r.sorted = reinterpret_cast<int16_t *>(lds);
+  r.routed = r.sorted + padded;
+  r.counts = reinterpret_cast<int *>(r.routed + padded);
+  r.base = r.counts + experts + 1;
+  return r;
+}
+
 template <bool kIds64, bool kWeights16>
-__device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShared &shared) {
+__device__ __forceinline__ void route_and_group(const PrepareArgs &a, const RouteShared &shared,
+                                                int *scratch) {
   int16_t *sorted = shared.sorted;
   int16_t *routed = shared.routed;
-  int *counts = shared.counts;
-  int *segment_count = shared.segment_count;
-  int *expert_tile = shared.expert_tile;
-  int *scratch = shared.scratch;
+  int *counts = shared.counts, *base = shared.base;
   const int tid = threadIdx.x;
   const int T = a.T, K = a.K;
   const int pairs = T * K;
-  constexpr int kPerThread = kMaxPairs / kPrepareThreads;
   auto weight_of = [&](int q) {
     return kWeights16 ? bf16f(load_global(static_cast<const uint16_t *>(a.router_weights) + q))
                       : load_global(static_cast<const float *>(a.router_weights) + q);
@@ -377,93 +390,64 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShare
   const int padded = (pairs + 7) / 8 * 8;
   for (int p = pairs + tid; p < padded; p += kPrepareThreads) sorted[p] = -1;
   __syncthreads();
-  // matches of expert e among pairs [begin, end) (multiples of 8)
-  auto matches = [&](int e, int begin, int end) {
-    int count = 0;
-    for (int p = begin; p < end; p += 8) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        count += static_cast<int16_t>(w[i] & 0xffffu) == e;
-        count += static_cast<int16_t>(w[i] >> 16) == e;
-      }
-    }
-    return count;
-  };
-  // place expert e's pairs among [begin, end) in order from tile slot `at`:
-  // tile z holds its pairs at group_pairs[16 z ..], and pair_tiles maps each
-  // placed pair back to its slot
-  auto place = [&](int e, int begin, int end, int at) {
-    for (int p = begin; p < end; p += 8) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(&sorted[p]);
-      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (static_cast<int16_t>(w[i] & 0xffffu) == e) {
-          a.group_pairs[at] = p + 2 * i;
-          a.pair_tiles[p + 2 * i] = at++;
-        }
-        if (static_cast<int16_t>(w[i] >> 16) == e) {
-          a.group_pairs[at] = p + 2 * i + 1;
-          a.pair_tiles[p + 2 * i + 1] = at++;
-        }
-      }
-    }
-  };
-  // tiles of at most kGroupPairs pairs, one screen workgroup each
-  auto emit_tiles = [&](int e, int count, int z) {
-    for (int first_pair = 0; first_pair < count; first_pair += kGroupPairs) {
-      a.group_experts[z] = e;
-      a.group_starts[z] = kGroupPairs * z;
-      a.group_counts[z] = min(kGroupPairs, count - first_pair);
-      ++z;
-    }
-  };
-  int total_tiles;
-  if (a.E <= kPrepareThreads) {
-    // `share` consecutive threads scan consecutive segments of the pairs for
-    // one expert: segment counts, an in-group prefix, ordered placement
-    int share = 1;
-    while (share * 2 * a.E <= kPrepareThreads) share *= 2;
-    const int e = tid / share, part = tid % share;
-    const int segment = (padded / 8 + share - 1) / share * 8;
-    const int begin = min(padded, part * segment), end = min(padded, begin + segment);
-    const int mine = e < a.E ? matches(e, begin, end) : 0;
-    segment_count[tid] = mine;
-    __syncthreads();
-    int before = 0, count = 0;
-    if (e < a.E)
-      for (int j = 0; j < share; ++j) {
-        const int c = segment_count[e * share + j];
-        before += j < part ? c : 0;
-        count += c;
-      }
-    const bool leader = e < a.E && part == 0;
-    int z = block_exclusive(leader ? (count + kGroupPairs - 1) / kGroupPairs : 0, scratch,
-                            &total_tiles);
-    if (leader) expert_tile[e] = z;
-    __syncthreads();
-    if (e < a.E && mine > 0) place(e, begin, end, kGroupPairs * expert_tile[e] + before);
-    if (leader && count > 0) emit_tiles(e, count, z);
-  } else {
-    // each thread owns the contiguous experts [first, last)
-    const int span = (a.E + kPrepareThreads - 1) / kPrepareThreads;
-    const int first = min(a.E, tid * span), last = min(a.E, first + span);
-    int tiles = 0;
-    for (int e = first; e < last; ++e) {
-      const int count = matches(e, 0, padded);
-      counts[e] = count;
-      tiles += (count + kGroupPairs - 1) / kGroupPairs;
-    }
-    int z = block_exclusive(tiles, scratch, &total_tiles);
+  // Expert-major grouping as a counting sort by expert, stable in pair order:
+  // (1) per-expert counts; (2) one scan of packed (members, tiles) gives each
+  // expert its member start and first tile z_e, and its tiles are emitted;
+  // (3) pairs drop into per-expert buckets (any order); (4) a pair's final
+  // slot is 16 z_e + its rank by pair index within its bucket.
+  for (int e = tid; e <= a.E; e += kPrepareThreads) counts[e] = 0;
+  __syncthreads();
+  for (int p = tid; p < pairs; p += kPrepareThreads) {
+    const int e = sorted[p];
+    if (e >= 0) atomicAdd(&counts[e], 1);
+  }
+  __syncthreads();
+  // thread i owns the experts [i per, (i + 1) per)
+  const int per = (a.E + kPrepareThreads - 1) / kPrepareThreads;
+  const int first = min(a.E, tid * per), last = min(a.E, first + per);
+  int members = 0, tiles = 0;
+  for (int e = first; e < last; ++e) {
+    members += counts[e];
+    tiles += (counts[e] + kGroupPairs - 1) / kGroupPairs;
+  }
+  int packed_total;  // members and tiles are below 2^16 (pairs <= 8192)
+  const int packed = block_exclusive(members | (tiles << 16), scratch, &packed_total);
+  const int total_tiles = packed_total >> 16;
+  {
+    int start = packed & 0xffff, z = packed >> 16;
     for (int e = first; e < last; ++e) {
       const int count = counts[e];
-      if (count == 0) continue;
-      place(e, 0, padded, kGroupPairs * z);
-      emit_tiles(e, count, z);
-      z += (count + kGroupPairs - 1) / kGroupPairs;
+      base[e] = start | (z << 16);
+      for (int first_pair = 0; first_pair < count; first_pair += kGroupPairs) {
+        a.group_experts[z] = e;
+        a.group_starts[z] = kGroupPairs * z;
+        a.group_counts[z] = min(kGroupPairs, count - first_pair);
+        ++z;
+      }
+      start += count;
     }
+    if (tid == kPrepareThreads - 1) base[a.E] = packed_total & 0xffff;
+  }
+  __syncthreads();
+  // bucket cursors start at each expert's member start
+  for (int e = tid; e < a.E; e += kPrepareThreads) counts[e] = base[e] & 0xffff;
+  __syncthreads();
+  int16_t *bucket = routed;
+  for (int p = tid; p < pairs; p += kPrepareThreads) {
+    const int e = sorted[p];
+    if (e >= 0) bucket[atomicAdd(&counts[e], 1)] = static_cast<int16_t>(p);
+  }
+  __syncthreads();
+  for (int p = tid; p < pairs; p += kPrepareThreads) {
+    const int e = sorted[p];
+    if (e < 0) continue;
+    const int begin = base[e] & 0xffff, end = base[e + 1] & 0xffff, z = base[e] >> 16;
+    int rank = 0;
+#pragma unroll 8
+    for (int j = begin; j < end; ++j) rank += bucket[j] < p;
+    const int at = kGroupPairs * z + rank;
+    a.group_pairs[at] = p;
+    a.pair_tiles[p] = at;
   }
   if (tid == 0) *a.group_total = total_tiles;
   // fixed read charges: one add per slot for all active tokens (integers, exact)
@@ -478,14 +462,16 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, RouteShare
 
 __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
   // block 0 routes and groups (the longest block, dispatched first)
-  __shared__ RouteShared route_shared;
+  extern __shared__ __align__(16) char route_lds[];
+  __shared__ int route_scratch[32];
   if (a.route && blockIdx.x == 0) {
+    const RouteShared shared = route_layout(route_lds, a.T * a.K, a.E);
     if (a.flags & CFMOE_IDS_INT64) {
-      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<true, true>(a, route_shared);
-      else route_and_group<true, false>(a, route_shared);
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<true, true>(a, shared, route_scratch);
+      else route_and_group<true, false>(a, shared, route_scratch);
     } else {
-      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<false, true>(a, route_shared);
-      else route_and_group<false, false>(a, route_shared);
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<false, true>(a, shared, route_scratch);
+      else route_and_group<false, false>(a, shared, route_scratch);
     }
     return;
   }
@@ -1722,8 +1708,9 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.rotate = rotate;
   a.cells = tokens * (rotate ? s.B : 1);
   const int cell_blocks = (a.cells + 3) / 4;
-  hipLaunchKernelGGL(prepare_kernel, dim3(cell_blocks + (route ? 1 : 0)), dim3(kPrepareThreads), 0,
-                     stream, a);
+  const long lds = route ? route_lds_bytes(tokens * s.K, d->experts) : 0;
+  hipLaunchKernelGGL(prepare_kernel, dim3(cell_blocks + (route ? 1 : 0)), dim3(kPrepareThreads),
+                     static_cast<unsigned>(lds), stream, a);
   return check_launch("prepare");
 }
 
