@@ -1482,25 +1482,29 @@ struct OutputArgs {
   float *latent;
   uint16_t *out;
   int H, K, R, max_tiles, encoder_tiles;
+  int columns;  // outputs per workgroup (64 or 256, at most kOutputThreads)
 };
 
 constexpr int kGroupExactTokens = 16;  // batches that use group_exact_kernel
-constexpr int kOutputColumns = 64;   // outputs per workgroup
 constexpr int kOutputThreads = 512;
 constexpr int kMaxEncoderTiles = 16; // ceil(I / 64) at I <= 1024
 constexpr int kTileBatch = 8;        // tile partials loaded together per thread
 
-// Workgroup = 64 outputs of one token, 512 threads. Thread (slot k, output)
-// sums the slot's 16-channel tile partials in tile order (all loads of a
-// batch issued together) and rounds to BF16; 64 threads then mix the slots
-// in order with the router weights and add the decoder correction.
+// Workgroup = `columns` outputs of one token, 512 threads (64 outputs below
+// 16 tokens for latency, 256 from there: every workgroup folds its token's
+// encoder tiles, so fewer, wider workgroups read them fewer times). Thread
+// item (slot k, output) sums the slot's 16-channel tile partials in tile order
+// (all loads of a batch issued together) and rounds to BF16; one thread per
+// output then mixes the slots in order with the router weights and adds the
+// decoder correction. The per-(slot, output) values live in dynamic LDS.
 __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   __shared__ float slot_latent[kMaxSlots * kMaxRank];
   __shared__ float latent[kMaxRank];
-  __shared__ float slot_value[kMaxSlots][kOutputColumns];
   __shared__ float slot_weight[kMaxSlots];
+  extern __shared__ float slot_value[];  // [K][columns]
   const int t = blockIdx.y, tid = threadIdx.x;
-  const int o0 = blockIdx.x * kOutputColumns;
+  const int columns = a.columns;
+  const int o0 = blockIdx.x * columns;
   const int K = a.K, R = a.R;
   for (int k = tid; k < K; k += kOutputThreads) slot_weight[k] = a.weights[t * K + k];
   // each slot's encoder tiles summed in tile order, rounded to BF16
@@ -1517,8 +1521,8 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
     slot_latent[k * R + r] = bfr(total);
   }
   // each slot's down tiles summed in tile order, rounded to BF16
-  for (int item = tid; item < K * kOutputColumns; item += kOutputThreads) {
-    const int k = item / kOutputColumns, column = item % kOutputColumns;
+  for (int item = tid; item < K * columns; item += kOutputThreads) {
+    const int k = item / columns, column = item % columns;
     const int o = o0 + column;
     const int first = a.down_tile_starts[t * K + k];
     const int tiles = min((a.counts[t * K + k] + 15) / 16, a.max_tiles - first);
@@ -1534,7 +1538,7 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
       for (int j = 0; j < kTileBatch; ++j)
         if (j0 + j < tiles) total = j0 + j == 0 ? v[j] : total + v[j];
     }
-    slot_value[k][column] = bfr(total);
+    slot_value[k * columns + column] = bfr(total);
   }
   __syncthreads();
   if (tid < R) {
@@ -1545,9 +1549,9 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   }
   __syncthreads();
   const int o = o0 + tid;
-  if (tid >= kOutputColumns || o >= a.H) return;
+  if (tid >= columns || o >= a.H) return;
   float routed = 0.0f;
-  for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k][tid], slot_weight[k], routed);
+  for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k * columns + tid], slot_weight[k], routed);
   float correction = 0.0f;
   if (R > 0 && a.decoder) {
     const bool active = is_active(a.padding, t);
@@ -2058,8 +2062,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.R = s.R;
   op.max_tiles = s.max_tiles;
   op.encoder_tiles = s.encoder_tiles;
-  hipLaunchKernelGGL(output_kernel, dim3((s.H + kOutputColumns - 1) / kOutputColumns, tokens),
-                     dim3(kOutputThreads), 0, stream, op);
+  op.columns = tokens >= kGroupExactTokens && s.K <= 16 ? 256 : 64;  // LDS <= 16 KB
+  hipLaunchKernelGGL(output_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
+                     dim3(kOutputThreads), static_cast<unsigned>(s.K * op.columns * sizeof(float)),
+                     stream, op);
   return check_launch("output");
 }
 
