@@ -792,17 +792,16 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
 
   // ---- B operands and per-pair constants of this lane's pair column
   const int pp = lane % 16, k0 = 16 * (lane / 16);
-  v4i operand[kMaxSpan][2][3];
+  // B operands are read from LDS per row tile (holding all twelve would
+  // cost 48 registers and half the waves per SIMD)
+  auto operand = [&](int bl, int h, int d) {
+    return *reinterpret_cast<const v4i *>(&sh.digits[bl][d][pp][64 * h + k0]);
+  };
   v4i start[kMaxSpan];
   int shift[kMaxSpan];
   float norm2[kMaxSpan];
 #pragma unroll
   for (int bl = 0; bl < kMaxSpan; ++bl) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int d = 0; d < 3; ++d)
-        operand[bl][h][d] = *reinterpret_cast<const v4i *>(&sh.digits[bl][d][pp][64 * h + k0]);
     const int qsum = sh.qsum[bl][pp];
     start[bl] = v4i{-qsum, -qsum, -qsum, -qsum};
     shift[bl] = sh.shift[bl][pp];
@@ -821,14 +820,14 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
       const v4i a0 = expand_digits(tile.words[bl].x);
       const v4i a1 = expand_digits(tile.words[bl].y);
       v4i acc[3];
-      acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][0], start[bl], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][1], v4i{0, 0, 0, 0}, 0,
+      acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand(bl, 0, 0), start[bl], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand(bl, 0, 1), v4i{0, 0, 0, 0}, 0,
                                                      0, 0);
-      acc[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand[bl][0][2], v4i{0, 0, 0, 0}, 0,
+      acc[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand(bl, 0, 2), v4i{0, 0, 0, 0}, 0,
                                                      0, 0);
 #pragma unroll
       for (int d = 0; d < 3; ++d)
-        acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, operand[bl][1][d], acc[d], 0, 0, 0);
+        acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, operand(bl, 1, d), acc[d], 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int sum = acc[0][r] + (acc[1][r] << 8) + (acc[2][r] << 16);
