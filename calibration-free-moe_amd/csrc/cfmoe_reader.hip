@@ -995,6 +995,7 @@ __device__ __forceinline__ int select_find_bin(const int *histogram, int bins, i
   return owner_top - 1 - at;
 }
 
+template <int kKeys>  // keys per thread: N <= kKeys * kSelectThreads
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int histogram[3][kSelectSlots];
   __shared__ int scratch[32];
@@ -1008,10 +1009,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
   // keys: every load issued unconditionally (absent keys read a zero)
-  uint32_t key[kSelectKeys];
+  uint32_t key[kKeys];
   const float *row = a.scores + static_cast<long>(t) * a.N;
 #pragma unroll
-  for (int j = 0; j < kSelectKeys; ++j) {
+  for (int j = 0; j < kKeys; ++j) {
     const bool present = j < per && first + j < a.N;
     const float *source =
         present ? row + first + j : reinterpret_cast<const float *>(&kZeroVector);
@@ -1023,7 +1024,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
     const uint32_t bound = __float_as_uint(*a.threshold + 0.0f);
     int passing = 0;
 #pragma unroll
-    for (int j = 0; j < kSelectKeys; ++j) passing += valid(j) && key[j] >= bound;
+    for (int j = 0; j < kKeys; ++j) passing += valid(j) && key[j] >= bound;
     passing = block_sum(passing, scratch);
     want = min(want, passing);
   } else {
@@ -1040,7 +1041,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
       const int shift = shifts[pass];
       const uint32_t bins = 1u << widths[pass];
 #pragma unroll
-      for (int j = 0; j < kSelectKeys; ++j)
+      for (int j = 0; j < kKeys; ++j)
         if (valid(j) && (key[j] & mask) == prefix)
           atomicAdd(&histogram[pass][select_slot((key[j] >> shift) & (bins - 1))], 1);
       __syncthreads();
@@ -1066,7 +1067,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int room = want;
   int above_here = 0, tied_here = 0;
 #pragma unroll
-  for (int j = 0; j < kSelectKeys; ++j) {
+  for (int j = 0; j < kKeys; ++j) {
     above_here += any && valid(j) && key[j] > cutoff;
     tied_here += any && valid(j) && key[j] == cutoff;
   }
@@ -1075,7 +1076,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
   int above_before = packed & 0xffff, tied_before = packed >> 16;
 #pragma unroll
-  for (int j = 0; j < kSelectKeys; ++j) {
+  for (int j = 0; j < kKeys; ++j) {
     if (!valid(j)) continue;
     const int i = first + j;
     bool keep = false;
@@ -1940,7 +1941,11 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       if ((rc = check_launch("score"))) return rc;
     }
     if (stages & (1u << CFMOE_STAGE_SELECT)) {
-      hipLaunchKernelGGL(select_kernel, dim3(tokens), dim3(kSelectThreads), 0, stream, sel);
+      if (s.N <= 8 * kSelectThreads)
+        hipLaunchKernelGGL(select_kernel<8>, dim3(tokens), dim3(kSelectThreads), 0, stream, sel);
+      else
+        hipLaunchKernelGGL(select_kernel<kSelectKeys>, dim3(tokens), dim3(kSelectThreads), 0,
+                           stream, sel);
       if ((rc = check_launch("select"))) return rc;
     }
   } else if (stages & (1u << CFMOE_STAGE_SELECT)) {
