@@ -1139,6 +1139,94 @@ __global__ void select_all_kernel(SelectArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// encode (progressive.py:1859-1951): skipped channels of a 64-channel tile
+
+struct EncodeArgs {
+  const uint16_t *encoder_t;
+  const float *partial;
+  const uint16_t *activations;
+  const uint8_t *completed;
+  const uint8_t *selected;
+  const int32_t *ids;
+  const uint8_t *padding;
+  float *parts;
+  int I, K, N, R, tiles, gelu;
+};
+
+constexpr int kEncodeStride = 72;  // LDS row stride (bf16) of a staged encoder row
+
+// One (64-channel tile, slot, token) item on one wave; `coefficients` is the
+// wave's own LDS slice of 64 rows of `stride` bf16. Every wave of the
+// workgroup calls it (its barrier is the workgroup's); `store` is false for a
+// wave whose item is past the work (it runs on a clamped item, stores nothing).
+__device__ __forceinline__ void encode_tile(const EncodeArgs &a, int tile, int k, int t,
+                                            bool store, uint16_t *coefficients, int stride) {
+  const int lane = threadIdx.x & 63;
+  const int c = tile * 64 + lane;
+  const int e = a.ids[t * a.K + k];
+  const bool local = is_active(a.padding, t) && e >= 0;
+  // every load issued unconditionally (clamped channel, zero row source)
+  const int cc = min(c, a.I - 1);
+  const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + cc;
+  const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + cc;
+  const uint8_t is_selected = load_global(a.selected + flat);
+  const uint8_t is_completed = load_global(a.completed + flat);
+  const uint16_t exact = load_global(a.activations + flat);
+  const float gate = load_global(a.partial + base);
+  const float up = load_global(a.partial + base + a.N);
+  const bool rows16 = (a.R & 7) == 0;
+  uint4 coefficient_rows[kMaxRank / 8];
+  const uint16_t *row = a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + cc) * a.R;
+  if (rows16) {
+#pragma unroll
+    for (int q = 0; q < kMaxRank / 8; ++q) {
+      const uint4 *source = (local && 8 * q < a.R) ? reinterpret_cast<const uint4 *>(row + 8 * q)
+                                                   : &kZeroVector;
+      coefficient_rows[q] = load_global(source);
+    }
+  }
+  const int skip = c < a.I && !is_selected;
+  float v = 0.0f;
+  if (skip)
+    v = is_completed ? bf16f(exact) : bfr(cfm_activate(bfr(gate), a.gelu != 0) * bfr(up));
+  uint16_t *staged = &coefficients[lane * stride];
+  if (rows16) {
+#pragma unroll
+    for (int q = 0; q < kMaxRank / 8; ++q)
+      if (8 * q < a.R) *reinterpret_cast<uint4 *>(staged + 8 * q) = coefficient_rows[q];
+  } else if (skip && local) {
+    for (int q = 0; q < a.R; ++q) staged[q] = row[q];
+  }
+  const uint64_t skipped = __ballot(skip);
+  __syncthreads();
+  // lane r < R: chain over the tile's skipped channels in order; a kept
+  // channel leaves the sum untouched (a select, not an added zero), so the
+  // loop has no branch and its LDS reads issue together (lanes >= R read
+  // in-bounds staged columns and store nothing)
+  float acc = 0.0f;
+  const int column = min(lane, stride - 1);
+#pragma unroll
+  for (int j = 0; j < 64; ++j) {
+    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+    const float coefficient = local ? bf16f(coefficients[j * stride + column]) : 0.0f;
+    const float next = fmaf(value, coefficient, acc);
+    acc = (skipped >> j) & 1ull ? next : acc;
+  }
+  if (store && lane < a.R)
+    a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * a.R + lane] = acc;
+}
+
+// LDS row stride (bf16) of a wave's staged encoder rows when encode runs
+// inside the exact kernels (sized by R: the exact workgroups share the launch)
+__host__ __device__ inline int encode_stride(int R) { return (R + 7) / 8 * 8 + 8; }
+constexpr int kEncodeWaves = 4;  // encode items per 256-thread workgroup of the exact kernels
+
+__global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
+  __shared__ __align__(16) uint16_t coefficients[64 * kEncodeStride];
+  encode_tile(a, blockIdx.x, blockIdx.y, blockIdx.z, true, coefficients, kEncodeStride);
+}
+
+// ---------------------------------------------------------------------------
 // exact (progressive.py:1510-1546): one wave per kept channel
 
 struct ExactArgs {
@@ -1151,10 +1239,35 @@ struct ExactArgs {
   uint16_t *activations;
   uint8_t *completed;
   int H, I, K, N, F, gelu;
+  // encode items run by the workgroups past exact_blocks (0: none); encode
+  // reads no exact result (a skipped channel is never completed)
+  EncodeArgs encode;
+  int exact_blocks, encode_items;
 };
+
+// Workgroups of an exact kernel past its own work run four encode items
+// (one per wave) from the launch's dynamic LDS.
+// `item` enumerates (tile, slot, token) tile-fastest; a wave past the work
+// runs a valid (clamped) item and stores nothing.
+__device__ __forceinline__ void encode_in_exact(const EncodeArgs &enc, int item, bool store) {
+  extern __shared__ __align__(16) uint16_t encode_lds[];
+  const int wave = threadIdx.x >> 6;
+  const int stride = encode_stride(enc.R);
+  const int tile = item % enc.tiles, rest = item / enc.tiles;
+  const int k = rest % enc.K, t = rest / enc.K;
+  encode_tile(enc, tile, k, t, store, encode_lds + wave * 64 * stride, stride);
+}
 
 __global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (static_cast<int>(blockIdx.x) >= a.exact_blocks) {
+    // this token's encode items
+    const int per_token = a.encode.tiles * a.encode.K;
+    const int local_item = (blockIdx.x - a.exact_blocks) * kEncodeWaves + wave;
+    encode_in_exact(a.encode, blockIdx.y * per_token + min(local_item, per_token - 1),
+                    local_item < per_token);
+    return;
+  }
   const int f = blockIdx.x * 4 + wave;
   const int t = blockIdx.y;
   if (f >= a.F) return;
@@ -1313,79 +1426,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void g
     uu = wave_sum_lane0(uu);
     if (lane == 0) exact_results(a, t, target, g, uu);
   }
-}
-
-// ---------------------------------------------------------------------------
-// encode (progressive.py:1859-1951): skipped channels of a 64-channel tile
-
-struct EncodeArgs {
-  const uint16_t *encoder_t;
-  const float *partial;
-  const uint16_t *activations;
-  const uint8_t *completed;
-  const uint8_t *selected;
-  const int32_t *ids;
-  const uint8_t *padding;
-  float *parts;
-  int I, K, N, R, tiles, gelu;
-};
-
-constexpr int kEncodeStride = 72;  // LDS row stride (bf16) of a staged encoder row
-
-__global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
-  __shared__ __align__(16) uint16_t coefficients[64 * kEncodeStride];
-  const int tile = blockIdx.x, k = blockIdx.y, t = blockIdx.z, lane = threadIdx.x;
-  const int c = tile * 64 + lane;
-  const long logical = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + c;
-  const int e = a.ids[t * a.K + k];
-  const bool local = is_active(a.padding, t) && e >= 0;
-  // every load issued unconditionally (clamped channel, zero row source)
-  const int cc = min(c, a.I - 1);
-  const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + cc;
-  const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + cc;
-  const uint8_t is_selected = load_global(a.selected + flat);
-  const uint8_t is_completed = load_global(a.completed + flat);
-  const uint16_t exact = load_global(a.activations + flat);
-  const float gate = load_global(a.partial + base);
-  const float up = load_global(a.partial + base + a.N);
-  const bool rows16 = (a.R & 7) == 0;
-  uint4 coefficient_rows[kMaxRank / 8];
-  const uint16_t *row = a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + cc) * a.R;
-  if (rows16) {
-#pragma unroll
-    for (int q = 0; q < kMaxRank / 8; ++q) {
-      const uint4 *source = (local && 8 * q < a.R) ? reinterpret_cast<const uint4 *>(row + 8 * q)
-                                                   : &kZeroVector;
-      coefficient_rows[q] = load_global(source);
-    }
-  }
-  const int skip = c < a.I && !is_selected;
-  float v = 0.0f;
-  if (skip)
-    v = is_completed ? bf16f(exact) : bfr(cfm_activate(bfr(gate), a.gelu != 0) * bfr(up));
-  uint16_t *staged = &coefficients[lane * kEncodeStride];
-  if (rows16) {
-#pragma unroll
-    for (int q = 0; q < kMaxRank / 8; ++q)
-      if (8 * q < a.R) *reinterpret_cast<uint4 *>(staged + 8 * q) = coefficient_rows[q];
-  } else if (skip && local) {
-    for (int q = 0; q < a.R; ++q) staged[q] = row[q];
-  }
-  const uint64_t skipped = __ballot(skip);
-  __syncthreads();
-  // lane r < R: chain over the tile's skipped channels in order; a kept
-  // channel leaves the sum untouched (a select, not an added zero), so the
-  // loop has no branch and its LDS reads issue together (lanes >= R compute
-  // on their in-bounds staged columns and store nothing)
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 64; ++j) {
-    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-    const float coefficient = local ? bf16f(coefficients[j * kEncodeStride + lane]) : 0.0f;
-    const float next = fmaf(value, coefficient, acc);
-    acc = (skipped >> j) & 1ull ? next : acc;
-  }
-  if (lane < a.R) a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * a.R + lane] = acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -1954,6 +1994,31 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     if ((rc = check_launch("select_all"))) return rc;
   }
 
+  EncodeArgs en;
+  memset(&en, 0, sizeof(en));
+  en.encoder_t = static_cast<const uint16_t *>(weights->encoder_t);
+  en.partial = workspace->partial;
+  en.activations = static_cast<const uint16_t *>(workspace->activations);
+  en.completed = workspace->completed;
+  en.selected = workspace->selected;
+  en.ids = workspace->ids;
+  en.padding = padding;
+  en.parts = workspace->encoder_parts;
+  en.I = s.I;
+  en.K = s.K;
+  en.N = s.N;
+  en.R = s.R;
+  en.tiles = s.encoder_tiles;
+  en.gelu = gelu;
+  // small batches run the encoder inside the per-token exact launch (one launch
+  // fewer); the grouped launch keeps it separate, since the encoder's dynamic
+  // LDS would apply to every exact workgroup and halve their occupancy
+  const bool fuse_encode = s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) &&
+                           (stages & (1u << CFMOE_STAGE_EXACT)) && tokens < kGroupExactTokens;
+  const int encode_items = fuse_encode ? s.encoder_tiles * s.K * tokens : 0;
+  const unsigned encode_lds =
+      fuse_encode ? static_cast<unsigned>(kEncodeWaves * 64 * encode_stride(s.R) * 2) : 0u;
+
   ExactArgs ex;
   ex.gate_up = static_cast<const uint16_t *>(weights->gate_up);
   ex.x = static_cast<const uint16_t *>(hidden);
@@ -2002,27 +2067,20 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + tokens), dim3(256), 0, stream,
                          gx);
     } else {
-      hipLaunchKernelGGL(exact_kernel, dim3((s.F + 3) / 4, tokens), dim3(256), 0, stream, ex);
+      ex.encode = en;
+      ex.encode_items = encode_items;
+      ex.exact_blocks = (s.F + 3) / 4;
+      const int encode_blocks =
+          fuse_encode ? (s.encoder_tiles * s.K + kEncodeWaves - 1) / kEncodeWaves : 0;
+      hipLaunchKernelGGL(exact_kernel, dim3(ex.exact_blocks + encode_blocks, tokens), dim3(256),
+                         encode_lds, stream, ex);
     }
     if ((rc = check_launch("exact"))) return rc;
   }
 
-  if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE))) {
-    EncodeArgs en;
-    en.encoder_t = static_cast<const uint16_t *>(weights->encoder_t);
-    en.partial = workspace->partial;
-    en.activations = static_cast<const uint16_t *>(workspace->activations);
-    en.completed = workspace->completed;
-    en.selected = workspace->selected;
-    en.ids = workspace->ids;
-    en.padding = padding;
-    en.parts = workspace->encoder_parts;
-    en.I = s.I;
-    en.K = s.K;
-    en.N = s.N;
-    en.R = s.R;
-    en.tiles = s.encoder_tiles;
-    en.gelu = gelu;
+  // encode runs inside the per-token exact launch when a call has both stages;
+  // otherwise (grouped batches, cfmoe_launch_stage) it is its own kernel
+  if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) && !fuse_encode) {
     hipLaunchKernelGGL(encode_kernel, dim3(s.encoder_tiles, s.K, tokens), dim3(64), 0, stream, en);
     if ((rc = check_launch("encode"))) return rc;
   }
