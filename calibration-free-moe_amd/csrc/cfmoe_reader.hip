@@ -157,6 +157,25 @@ __device__ __forceinline__ uint2 load_global(const uint2 *p) {
 // Load source of dead lanes (no branch around a load, no select after it).
 __device__ const uint4 kZeroVector = {0, 0, 0, 0};
 
+// Raw buffer resource over `bytes` bytes from a wave-uniform base (stride 0,
+// the gfx9 default format word): a buffer load past `bytes` reads zeros, and
+// every load of the wave shares one 32-bit lane offset (constant parts go into
+// the instruction's immediate offset), not a 64-bit address per load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_resource(const void *base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 buffer_load16(__amdgpu_buffer_rsrc_t r, int offset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// non-temporal (weights read once per call)
+__device__ __forceinline__ uint4 buffer_stream16(__amdgpu_buffer_rsrc_t r, int offset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 2);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint64_t lanes_below(int lane) {
   return lane == 0 ? 0ull : (~0ull >> (64 - lane));
 }
@@ -1355,8 +1374,13 @@ __device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, in
   a.completed[static_cast<long>(t) * a.N + logical] = 1;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void group_exact_kernel(
-    GroupExactArgs a) {
+// Waves per workgroup. One: a workgroup's waves are placed one per SIMD, so
+// a workgroup of several waves, whose lifetimes differ (channels that no pair
+// kept end at once), can start only when every SIMD of a CU has a free slot.
+constexpr int kGroupExactWaves = 1;
+
+__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(8))) void
+group_exact_kernel(GroupExactArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
     // zero results of a padded token or of a slot with no local expert
@@ -1366,7 +1390,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void g
     for (int k = 0; k < a.K; ++k) {
       if (active && a.ids[t * a.K + k] >= 0) continue;
       const int start = a.starts[t * a.K + k], count = a.counts[t * a.K + k];
-      for (int j = tid; j < count && start + j < a.F; j += 256) {
+      for (int j = tid; j < count && start + j < a.F; j += 64 * kGroupExactWaves) {
         const int logical = a.next_ids[static_cast<long>(t) * a.F + start + j];
         if (logical >= 0 && logical < a.N) exact_results(a, t, logical, 0.0f, 0.0f);
       }
@@ -1374,30 +1398,56 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void g
     return;
   }
   const int z = blockIdx.x / a.channel_groups;
-  const int c = (blockIdx.x % a.channel_groups) * 4 + wave;
-  if (z >= *a.group_total || c >= a.I) return;
-  const int e = a.group_experts[z], count = a.group_counts[z];
+  const int c =
+      __builtin_amdgcn_readfirstlane((blockIdx.x % a.channel_groups) * kGroupExactWaves + wave);
+  if (c >= a.I) return;
+  // The tile count, the tile's expert, pair count and 16 pair slots and this
+  // channel's mask are loaded in one round trip: z < tile bound <= T * K keeps
+  // every address in bounds whatever the tile count, and only slots named by
+  // mask bits (< count) are used.
+  const int total = __builtin_amdgcn_readfirstlane(load_global(a.group_total));
+  const int e = __builtin_amdgcn_readfirstlane(load_global(a.group_experts + z));
+  const int count = __builtin_amdgcn_readfirstlane(load_global(a.group_counts + z));
   // lane p < count: pair p of the tile
-  const int pair = a.group_pairs[kGroupPairs * z + min(lane, count - 1)];
-  const int token = pair / a.K, logical = (pair % a.K) * a.I + c;
-  const uint64_t mask =
-      a.dense ? (1ull << count) - 1ull : a.tile_masks[static_cast<long>(z) * a.I + c];
+  const int pair = load_global(a.group_pairs + kGroupPairs * z + (lane & (kGroupPairs - 1)));
+  const uint32_t mask_word =
+      a.dense ? 0u
+              : __builtin_amdgcn_readfirstlane(
+                    load_global(a.tile_masks + static_cast<long>(z) * a.I + c));
+  if (z >= total) return;
+  const uint32_t mask = a.dense ? (1u << count) - 1u : mask_word;  // count <= 16
   if (!mask) return;
-  const uint16_t *grow = a.gate_up + (static_cast<long>(e) * 2 * a.I + c) * a.H;
-  const uint16_t *urow = grow + static_cast<long>(a.I) * a.H;
+  const int token = pair / a.K, logical = (pair % a.K) * a.I + c;
+  // rows and hidden rows through buffer resources: lane offset 16 lane, part j
+  // at 1024 j bytes; parts past H read zeros and their chains are discarded
+  const int row_bytes = 2 * a.H, offset = 16 * lane;
+  const long grow = (static_cast<long>(e) * 2 * a.I + c) * a.H;
+  const __amdgpu_buffer_rsrc_t gate_rows = buffer_resource(a.gate_up + grow, row_bytes);
+  const __amdgpu_buffer_rsrc_t up_rows =
+      buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
   constexpr int kParts = kMaxHidden / 512;
+  uint4 xw[kParts];
+  auto load_hidden = [&](int pp) {
+    const int t = __builtin_amdgcn_readlane(token, pp);
+    const __amdgpu_buffer_rsrc_t hidden =
+        buffer_resource(a.x + static_cast<long>(t) * a.H, row_bytes);
+#pragma unroll
+    for (int j = 0; j < kParts; ++j) xw[j] = buffer_load16(hidden, offset + 1024 * j);
+  };
+  // the first keeping pair's hidden row travels with the gate/up rows
+  load_hidden(__builtin_ctz(mask));
   uint4 gw[kParts], uw[kParts];
 #pragma unroll
   for (int j = 0; j < kParts; ++j) {
-    const int h = min(512 * j + 8 * lane, a.H - 8);
-    gw[j] = load_stream16(grow + h);
-    uw[j] = load_stream16(urow + h);
+    gw[j] = buffer_stream16(gate_rows, offset + 1024 * j);
+    uw[j] = buffer_stream16(up_rows, offset + 1024 * j);
   }
-  for (uint64_t rest = mask; rest; rest &= rest - 1) {
-    const int pp = __builtin_ctzll(rest);
-    const int t = __shfl(token, pp);
-    const int target = __shfl(logical, pp);
-    const uint16_t *xr = a.x + static_cast<long>(t) * a.H;
+  // lane p holds pair p's sums; the results are stored after the loop (a
+  // store inside it would delay the next pair's loads, which wait in order)
+  float kept_g = 0.0f, kept_u = 0.0f;
+  for (uint32_t rest = mask; rest; rest &= rest - 1) {
+    const int pp = __builtin_ctz(rest);
+    if (rest != mask) load_hidden(pp);
     float g = 0.0f, uu = 0.0f;
     // keep the rows packed across pairs (unpacking them once ahead of the
     // loop would hold 64 more registers and halve the waves per SIMD)
@@ -1407,25 +1457,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void g
                    "+v"(uw[j].x), "+v"(uw[j].y), "+v"(uw[j].z), "+v"(uw[j].w));
 #pragma unroll
     for (int j = 0; j < kParts; ++j) {
-      const int h = 512 * j + 8 * lane;
-      if (h >= a.H) continue;
-      const uint4 xw = *reinterpret_cast<const uint4 *>(xr + h);
+      const bool inside = 512 * j + 8 * lane < a.H;
       const uint32_t gv[4] = {gw[j].x, gw[j].y, gw[j].z, gw[j].w};
       const uint32_t uv[4] = {uw[j].x, uw[j].y, uw[j].z, uw[j].w};
-      const uint32_t xv[4] = {xw.x, xw.y, xw.z, xw.w};
+      const uint32_t xv[4] = {xw[j].x, xw[j].y, xw[j].z, xw[j].w};
+      float gj = g, uj = uu;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
-        g = fmaf(__uint_as_float(gv[i] << 16), x0, g);
-        g = fmaf(__uint_as_float(gv[i] & 0xffff0000u), x1, g);
-        uu = fmaf(__uint_as_float(uv[i] << 16), x0, uu);
-        uu = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, uu);
+        gj = fmaf(__uint_as_float(gv[i] << 16), x0, gj);
+        gj = fmaf(__uint_as_float(gv[i] & 0xffff0000u), x1, gj);
+        uj = fmaf(__uint_as_float(uv[i] << 16), x0, uj);
+        uj = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, uj);
       }
+      g = inside ? gj : g;
+      uu = inside ? uj : uu;
     }
     g = wave_sum_lane0(g);
     uu = wave_sum_lane0(uu);
-    if (lane == 0) exact_results(a, t, target, g, uu);
+    kept_g = lane == pp ? g : kept_g;
+    kept_u = lane == pp ? uu : kept_u;
   }
+  if (lane < kGroupPairs && ((mask >> lane) & 1u)) exact_results(a, token, logical, kept_g, kept_u);
 }
 
 // ---------------------------------------------------------------------------
@@ -2062,10 +2115,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       gx.F = s.F;
       gx.T = tokens;
       gx.gelu = gelu;
-      gx.channel_groups = (s.I + 3) / 4;
+      gx.channel_groups = (s.I + kGroupExactWaves - 1) / kGroupExactWaves;
       gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
-      hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + tokens), dim3(256), 0, stream,
-                         gx);
+      hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + tokens), dim3(64 * kGroupExactWaves),
+                         0, stream, gx);
     } else {
       ex.encode = en;
       ex.encode_items = encode_items;
