@@ -1245,6 +1245,70 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   encode_tile(a, blockIdx.x, blockIdx.y, blockIdx.z, true, coefficients, kEncodeStride);
 }
 
+// The same item without LDS, at R = kDirectRank: lane r + 32 h (h = 0, 1)
+// loads the coefficients E[32 h + i][r] (i < 32) at once (row offsets are
+// immediates); lanes r < 32 run the chain over the tile's first 32 channels,
+// lanes 32 + r continue it over the last 32 from lane r's sum. Same order and
+// roundings as encode_tile.
+constexpr int kDirectRank = 32;
+
+template <class Args>  // EncodeArgs, or the grouped exact launch's arguments
+__device__ __forceinline__ void encode_tile_direct(const Args &a, int tile, int k, int t) {
+  constexpr int R = kDirectRank;
+  const int lane = threadIdx.x & 63;
+  const int c = tile * 64 + lane;
+  const int e = __builtin_amdgcn_readfirstlane(load_global(a.ids + t * a.K + k));
+  const bool local = is_active(a.padding, t) && e >= 0;
+  // the tile's flags and values through buffer resources (one lane offset;
+  // channels past I read zeros and are not skipped)
+  const int rows = min(64, a.I - tile * 64);
+  const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + tile * 64;
+  const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + tile * 64;
+  const uint8_t is_selected =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.selected + flat, rows), lane, 0, 0);
+  const uint8_t is_completed =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.completed + flat, rows), lane, 0, 0);
+  const uint16_t exact = __builtin_amdgcn_raw_buffer_load_b16(
+      buffer_resource(a.activations + flat, 2 * rows), 2 * lane, 0, 0);
+  const float gate = __uint_as_float(
+      __builtin_amdgcn_raw_buffer_load_b32(buffer_resource(a.partial + base, 4 * rows), 4 * lane, 0, 0));
+  const float up = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+      buffer_resource(a.partial + base + a.N, 4 * rows), 4 * lane, 0, 0));
+  // the tile's rows of E (rows past I read zeros)
+  const int r = lane & 31, half = lane >> 5;
+  const __amdgpu_buffer_rsrc_t block = buffer_resource(
+      a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + tile * 64) * R, rows * R * 2);
+  uint16_t coefficient[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i)
+    coefficient[i] = __builtin_amdgcn_raw_buffer_load_b16(block, 2 * (32 * half * R + r) + 2 * i * R, 0, 0);
+  const int skip = c < a.I && !is_selected;
+  float v = 0.0f;
+  if (skip)
+    v = is_completed ? bf16f(exact) : bfr(cfm_activate(bfr(gate), a.gelu != 0) * bfr(up));
+  const uint64_t skipped = __ballot(skip);
+  // each step tests its bit of the skipped mask in place (the empty asm keeps
+  // the compiler from precomputing all 32 conditions into scalar registers)
+  uint32_t low = static_cast<uint32_t>(skipped), high = static_cast<uint32_t>(skipped >> 32);
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    asm volatile("" : "+s"(low));
+    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+    const float next = fmaf(value, local ? bf16f(coefficient[i]) : 0.0f, acc);
+    acc = (low >> i) & 1u ? next : acc;
+  }
+  acc = __shfl(acc, r);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    asm volatile("" : "+s"(high));
+    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32 + i));
+    const float next = fmaf(value, local ? bf16f(coefficient[i]) : 0.0f, acc);
+    acc = (high >> i) & 1u ? next : acc;
+  }
+  if (half == 1) a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * R + r] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // exact (progressive.py:1510-1546): one wave per kept channel
 
@@ -1360,6 +1424,10 @@ struct GroupExactArgs {
   uint8_t *completed;
   int H, I, K, N, F, T, gelu, channel_groups, tile_items;
   int dense;  // every channel kept by every pair (no tile masks)
+  // recovery encoder items (R = kDirectRank) run past the exact tiles
+  const uint16_t *encoder_t;
+  float *parts;  // encoder partials
+  int tiles, encode_items;
 };
 
 constexpr int kMaxHidden = 2048;
@@ -1383,8 +1451,16 @@ __global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_
 group_exact_kernel(GroupExactArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
+    const int item = blockIdx.x - a.tile_items;
+    if (item < a.encode_items) {
+      // recovery encoder item (tile, slot, token), tile fastest; it reads no
+      // exact result (a skipped channel is never completed)
+      const int tile = item % a.tiles, rest = item / a.tiles;
+      encode_tile_direct(a, tile, rest % a.K, rest / a.K);
+      return;
+    }
     // zero results of a padded token or of a slot with no local expert
-    const int t = blockIdx.x - a.tile_items;
+    const int t = item - a.encode_items;
     if (t >= a.T) return;
     const bool active = is_active(a.padding, t);
     for (int k = 0; k < a.K; ++k) {
@@ -2068,6 +2144,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   // LDS would apply to every exact workgroup and halve their occupancy
   const bool fuse_encode = s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) &&
                            (stages & (1u << CFMOE_STAGE_EXACT)) && tokens < kGroupExactTokens;
+  // grouped batches run the encoder inside the grouped exact launch when it
+  // needs no LDS (R = kDirectRank)
+  const bool fuse_direct = s.R == kDirectRank && (stages & (1u << CFMOE_STAGE_ENCODE)) &&
+                           (stages & (1u << CFMOE_STAGE_EXACT)) && tokens >= kGroupExactTokens;
   const int encode_items = fuse_encode ? s.encoder_tiles * s.K * tokens : 0;
   const unsigned encode_lds =
       fuse_encode ? static_cast<unsigned>(kEncodeWaves * 64 * encode_stride(s.R) * 2) : 0u;
@@ -2117,8 +2197,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       gx.gelu = gelu;
       gx.channel_groups = (s.I + kGroupExactWaves - 1) / kGroupExactWaves;
       gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
-      hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + tokens), dim3(64 * kGroupExactWaves),
-                         0, stream, gx);
+      gx.encoder_t = en.encoder_t;
+      gx.parts = en.parts;
+      gx.tiles = en.tiles;
+      gx.encode_items = fuse_direct ? s.encoder_tiles * s.K * tokens : 0;
+      hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + gx.encode_items + tokens),
+                         dim3(64 * kGroupExactWaves), 0, stream, gx);
     } else {
       ex.encode = en;
       ex.encode_items = encode_items;
@@ -2133,7 +2217,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
 
   // encode runs inside the per-token exact launch when a call has both stages;
   // otherwise (grouped batches, cfmoe_launch_stage) it is its own kernel
-  if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) && !fuse_encode) {
+  if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) && !fuse_encode && !fuse_direct) {
     hipLaunchKernelGGL(encode_kernel, dim3(s.encoder_tiles, s.K, tokens), dim3(64), 0, stream, en);
     if ((rc = check_launch("encode"))) return rc;
   }

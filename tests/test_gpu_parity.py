@@ -209,17 +209,20 @@ def test_hot_expert_splits_into_screen_tiles():
     assert sorted(seen) == list(range(tokens * top_k))
 
 
-@pytest.mark.parametrize("score", ["point", "recovery-aware"])
-def test_grouped_batch_paths_bit_exact(score):
+@pytest.mark.parametrize("score,rank,width", [("point", 16, 256), ("recovery-aware", 16, 256),
+                                              ("point", 32, 288), ("recovery-aware", 32, 256)])
+def test_grouped_batch_paths_bit_exact(score, rank, width):
     """Batches of 16 or more use the grouped exact rows and per-slot down
-    values; padded tokens and a non-local slot exercise their zero results."""
+    values; padded tokens and a non-local slot exercise their zero results.
+    At rank 32 the recovery encoder runs inside the grouped exact launch
+    (width 288: a last encoder tile of 32 channels)."""
     tokens, experts, top_k = 24, 16, 4
-    layer = make_layer(hidden=512, width=256, experts=experts, top_k=top_k, rank=16,
+    layer = make_layer(hidden=512, width=width, experts=experts, top_k=top_k, rank=rank,
                        tokens=tokens, seed=71)
     layer.ids[5, 2] = 99  # no local expert: reads nothing, contributes zero
     padding = torch.zeros(tokens, dtype=torch.bool)
     padding[[3, 10]] = True
-    plan = compile_budget(hidden_size=512, expert_width=256, top_k=top_k, retention=0.123,
+    plan = compile_budget(hidden_size=512, expert_width=width, top_k=top_k, retention=0.123,
                           screen_keep=0.625)
     reader = build(layer, plan, tokens, selection_score=score)
     out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights, padding)
