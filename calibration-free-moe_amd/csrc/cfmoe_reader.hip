@@ -157,6 +157,18 @@ __device__ __forceinline__ uint2 load_global(const uint2 *p) {
 // Load source of dead lanes (no branch around a load, no select after it).
 __device__ const uint4 kZeroVector = {0, 0, 0, 0};
 
+// Wave-uniform loads through the scalar data cache (constant address space):
+// for values an earlier launch wrote and this one only reads. They bypass the
+// vector memory queue, where under load a small read waits behind the
+// wave's neighbours' row loads.
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T *p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) T *>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
 // Raw buffer resource over `bytes` bytes from a wave-uniform base (stride 0,
 // the gfx9 default format word): a buffer load past `bytes` reads zeros, and
 // every load of the wave shares one 32-bit lane offset (constant parts go into
@@ -1478,19 +1490,21 @@ group_exact_kernel(GroupExactArgs a) {
       __builtin_amdgcn_readfirstlane((blockIdx.x % a.channel_groups) * kGroupExactWaves + wave);
   if (c >= a.I) return;
   // The tile count, the tile's expert, pair count and 16 pair slots and this
-  // channel's mask are loaded in one round trip: z < tile bound <= T * K keeps
-  // every address in bounds whatever the tile count, and only slots named by
-  // mask bits (< count) are used.
-  const int total = __builtin_amdgcn_readfirstlane(load_global(a.group_total));
-  const int e = __builtin_amdgcn_readfirstlane(load_global(a.group_experts + z));
-  const int count = __builtin_amdgcn_readfirstlane(load_global(a.group_counts + z));
-  // lane p < count: pair p of the tile
-  const int pair = load_global(a.group_pairs + kGroupPairs * z + (lane & (kGroupPairs - 1)));
-  const uint32_t mask_word =
-      a.dense ? 0u
-              : __builtin_amdgcn_readfirstlane(
-                    load_global(a.tile_masks + static_cast<long>(z) * a.I + c));
+  // channel's mask, through the scalar cache in one round trip: z < tile bound
+  // <= T * K keeps every address in bounds whatever the tile count, and only
+  // slots named by mask bits (< count) are used.
+  const int total = load_uniform(a.group_total);
+  const int e = load_uniform(a.group_experts + z);
+  const int count = load_uniform(a.group_counts + z);
+  const i32x16 slots = load_uniform(reinterpret_cast<const i32x16 *>(a.group_pairs + kGroupPairs * z));
+  const uint32_t mask_word = load_uniform(a.tile_masks + static_cast<long>(z) * a.I + c);
+  // all five issued before any is tested (else each waits under its branch)
+  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots), "s"(mask_word));
   if (z >= total) return;
+  // lane p < count: pair p of the tile
+  int pair = slots[0];
+#pragma unroll
+  for (int p = 1; p < kGroupPairs; ++p) pair = (lane & (kGroupPairs - 1)) == p ? slots[p] : pair;
   const uint32_t mask = a.dense ? (1u << count) - 1u : mask_word;  // count <= 16
   if (!mask) return;
   const int token = pair / a.K, logical = (pair % a.K) * a.I + c;
