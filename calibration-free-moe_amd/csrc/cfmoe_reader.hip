@@ -1030,13 +1030,12 @@ template <int kKeys>  // keys per thread: N <= kKeys * kSelectThreads
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int histogram[3][kSelectSlots];
   __shared__ int scratch[32];
-  __shared__ int slot_counts[64];
+  __shared__ int slot_start[65];
   __shared__ int slot_tiles[64];
   __shared__ int shared_bin, shared_above;
   const int t = blockIdx.x, tid = threadIdx.x;
   if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
   for (int i = tid; i < 3 * kSelectSlots; i += kSelectThreads) (&histogram[0][0])[i] = 0;
-  if (tid < 64) slot_counts[tid] = 0;
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
   // keys: every load issued unconditionally (absent keys read a zero)
@@ -1106,10 +1105,17 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int packed = block_exclusive(above_here | (tied_here << 16), scratch, &packed_total);
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
   int above_before = packed & 0xffff, tied_before = packed >> 16;
+  // the next slot start at or after this thread's first candidate
+  int next_slot = (first + a.I - 1) / a.I, boundary = next_slot * a.I;
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) {
     if (!valid(j)) continue;
     const int i = first + j;
+    // the first candidate of a slot: the kept ids before it start the slot
+    if (i == boundary) {
+      slot_start[next_slot++] = any ? min(above_before + min(tied_before, room), a.F) : 0;
+      boundary += a.I;
+    }
     bool keep = false;
     if (any && key[j] > cutoff) {
       keep = true;
@@ -1124,7 +1130,6 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
       if (position < a.F) {
         a.next_ids[static_cast<long>(t) * a.F + position] = i;
         const int k = i / a.I;
-        atomicAdd(&slot_counts[k], 1);
         // the channel's bit for this pair in its tile's mask (OR: any order)
         const int slot_tile = a.tile_masks ? slot_tiles[k] : -1;
         if (slot_tile >= 0)
@@ -1135,18 +1140,20 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   }
   for (int p = kept_total + tid; p < a.F; p += kSelectThreads)
     a.next_ids[static_cast<long>(t) * a.F + p] = -1;
+  if (tid == 0) slot_start[a.K] = min(kept_total, a.F);
   __syncthreads();
-  if (tid == 0) {
-    int start = 0, tile = 0, tile16 = 0;
-    for (int k = 0; k < a.K; ++k) {
-      const int count = slot_counts[k];
-      a.counts[t * a.K + k] = count;
-      a.starts[t * a.K + k] = start;
-      a.tile_starts[t * a.K + k] = tile;
-      a.down_tile_starts[t * a.K + k] = tile16;
-      start += count;
-      tile += (count + 127) / 128;
-      tile16 += (count + 15) / 16;
+  // wave 0: lane k writes slot k's count, start and tile starts (K <= 64)
+  if (tid < kWave) {
+    const bool slot = tid < a.K;
+    const int start = slot ? slot_start[tid] : 0;
+    const int count = slot ? slot_start[tid + 1] - start : 0;
+    const int tiles = (count + 127) / 128, tiles16 = (count + 15) / 16;
+    const int tile = wave_inclusive(tiles) - tiles, tile16 = wave_inclusive(tiles16) - tiles16;
+    if (slot) {
+      a.counts[t * a.K + tid] = count;
+      a.starts[t * a.K + tid] = start;
+      a.tile_starts[t * a.K + tid] = tile;
+      a.down_tile_starts[t * a.K + tid] = tile16;
     }
   }
 }
