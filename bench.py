@@ -132,10 +132,27 @@ def algorithmic_bytes(reader: ProgressiveReader, tokens: int) -> dict[str, int]:
 
 STAGE_BYTES = {"screen": ("sketch",), "exact": ("gate_up",), "down": ("down",),
                "encode": ("encoder",)}
+DIRECT_RANK = 32  # rank at which grouped batches run the encoder inside the exact launch
 STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "group_screen_kernel",
                  "score": "score_kernel", "select": "select_kernel", "exact": "exact_kernel",
                  "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
 GROUP_EXACT_TOKENS = 16  # batches from which the exact stage runs group_exact_kernel
+
+
+def encoder_in_exact(tokens: int, rank: int) -> bool:
+    """Whether the exact launch also runs the recovery encoder (the encode
+    stage then launches nothing)."""
+    return rank > 0 and (tokens < GROUP_EXACT_TOKENS or rank == DIRECT_RANK)
+
+
+def stage_bytes(stage: str, tokens: int, rank: int) -> tuple[str, ...]:
+    """Algorithmic byte groups read by a stage's launch."""
+    if encoder_in_exact(tokens, rank):
+        if stage == "exact":
+            return ("gate_up", "encoder")
+        if stage == "encode":
+            return ()
+    return STAGE_BYTES.get(stage, ())
 
 
 def stage_kernel(stage: str, tokens: int) -> str:
@@ -302,7 +319,7 @@ def run_config(name: str, args, device) -> dict:
         torch.cuda.synchronize()
         stage_us[stage] = begin.elapsed_time(end) * 1e3 / (repeats * layers)
     dominant = max(STAGE_BYTES, key=lambda s: stage_us[s])
-    dominant_bytes = sum(mean_bytes[key] for key in STAGE_BYTES[dominant])
+    dominant_bytes = sum(mean_bytes[key] for key in stage_bytes(dominant, tokens, rank))
     achieved = dominant_bytes / (stage_us[dominant] * 1e-6) / 1e9
     return {
         "name": name,

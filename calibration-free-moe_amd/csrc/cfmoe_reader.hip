@@ -2160,15 +2160,16 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   en.R = s.R;
   en.tiles = s.encoder_tiles;
   en.gelu = gelu;
-  // small batches run the encoder inside the per-token exact launch (one launch
-  // fewer); the grouped launch keeps it separate, since the encoder's dynamic
-  // LDS would apply to every exact workgroup and halve their occupancy
-  const bool fuse_encode = s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) &&
-                           (stages & (1u << CFMOE_STAGE_EXACT)) && tokens < kGroupExactTokens;
-  // grouped batches run the encoder inside the grouped exact launch when it
-  // needs no LDS (R = kDirectRank)
-  const bool fuse_direct = s.R == kDirectRank && (stages & (1u << CFMOE_STAGE_ENCODE)) &&
-                           (stages & (1u << CFMOE_STAGE_EXACT)) && tokens >= kGroupExactTokens;
+  // Where the encoder runs inside the exact launch, the exact stage launches
+  // it (also alone, through cfmoe_launch_stage) and the encode stage has no
+  // launch of its own: small batches run it in the per-token exact launch (one
+  // launch fewer); grouped batches run it in the grouped exact launch when it
+  // needs no LDS (R = kDirectRank; the LDS encoder's dynamic LDS would apply to
+  // every exact workgroup and halve their occupancy)
+  const bool small = tokens < kGroupExactTokens;
+  const bool encode_in_exact = s.R > 0 && (small || s.R == kDirectRank);
+  const bool fuse_encode = encode_in_exact && small && (stages & (1u << CFMOE_STAGE_EXACT));
+  const bool fuse_direct = encode_in_exact && !small && (stages & (1u << CFMOE_STAGE_EXACT));
   const int encode_items = fuse_encode ? s.encoder_tiles * s.K * tokens : 0;
   const unsigned encode_lds =
       fuse_encode ? static_cast<unsigned>(kEncodeWaves * 64 * encode_stride(s.R) * 2) : 0u;
@@ -2236,9 +2237,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     if ((rc = check_launch("exact"))) return rc;
   }
 
-  // encode runs inside the per-token exact launch when a call has both stages;
-  // otherwise (grouped batches, cfmoe_launch_stage) it is its own kernel
-  if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) && !fuse_encode && !fuse_direct) {
+  // otherwise (grouped batches at R != kDirectRank) it is its own kernel
+  if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) && !encode_in_exact) {
     hipLaunchKernelGGL(encode_kernel, dim3(s.encoder_tiles, s.K, tokens), dim3(64), 0, stream, en);
     if ((rc = check_launch("encode"))) return rc;
   }

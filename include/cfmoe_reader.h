@@ -53,8 +53,10 @@ typedef struct ihipStream_t *cfmoe_stream;
 #define CFMOE_STAGE_SCREEN 1  /* sketch projections per block split */
 #define CFMOE_STAGE_SCORE 2   /* split sums and channel scores */
 #define CFMOE_STAGE_SELECT 3  /* per-token top-F */
-#define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels */
-#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels */
+#define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels (and the encoder, below) */
+#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels; below 16 tokens
+                                 and at rank 32 it runs inside the exact launch, and this
+                                 stage launches nothing */
 #define CFMOE_STAGE_DOWN 6    /* down rows of kept channels */
 #define CFMOE_STAGE_OUTPUT 7  /* latent, decoder correction, router mix */
 #define CFMOE_STAGE_COUNT 8
