@@ -67,7 +67,7 @@ RADIX_CAPACITY = 128
 RADIX_TOKENS = 4
 SelectionScore = Literal["recovery-aware", "point"]
 # Kept-channel tile of the down kernel and of the reference's tile_starts.
-DOWN_TILE = 16
+DOWN_TILE = 32
 REFERENCE_DOWN_TILE = 128
 ENCODER_TILE = 64
 

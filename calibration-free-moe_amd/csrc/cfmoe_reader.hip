@@ -11,7 +11,7 @@
 //   select_kernel    per-token top-F (radix select + compaction) (:1584-1775)
 //   exact_kernel     native gate/up rows of kept channels         (:1372-1581)
 //   encode_kernel    recovery encoder over skipped channels       (:1859-2016)
-//   down_kernel      down rows of kept channels, 16-channel tiles (:1778-1856)
+//   down_kernel      down rows of kept channels, 32-channel tiles (:1778-1856)
 //   output_kernel    latent, decoder correction, router mix       (:2019-2111)
 //
 // Arithmetic contract (shared with the CPU oracle, oracle/cfmoe_oracle.c):
@@ -35,6 +35,7 @@ namespace cfmoe {
 constexpr int kWave = 64;
 constexpr int kMaxSlots = 64;  // top_k limit of the C-ABI
 constexpr int kMaxRank = 64;   // recovery rank limit of the C-ABI
+constexpr int kDownTile = 32;  // selected channels per down tile (one fp32 partial each)
 
 // ---------------------------------------------------------------------------
 // scalar helpers (identical formulas in oracle/cfmoe_oracle.c)
@@ -1147,7 +1148,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
     const bool slot = tid < a.K;
     const int start = slot ? slot_start[tid] : 0;
     const int count = slot ? slot_start[tid + 1] - start : 0;
-    const int tiles = (count + 127) / 128, tiles16 = (count + 15) / 16;
+    const int tiles = (count + 127) / 128, tiles16 = (count + kDownTile - 1) / kDownTile;
     const int tile = wave_inclusive(tiles) - tiles, tile16 = wave_inclusive(tiles16) - tiles16;
     if (slot) {
       a.counts[t * a.K + tid] = count;
@@ -1171,7 +1172,7 @@ __global__ void select_all_kernel(SelectArgs a) {
       a.counts[t * a.K + k] = a.I;
       a.starts[t * a.K + k] = k * a.I;
       a.tile_starts[t * a.K + k] = k * ((a.I + 127) / 128);
-      a.down_tile_starts[t * a.K + k] = k * ((a.I + 15) / 16);
+      a.down_tile_starts[t * a.K + k] = k * ((a.I + kDownTile - 1) / kDownTile);
     }
   }
 }
@@ -1579,7 +1580,7 @@ group_exact_kernel(GroupExactArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// down (progressive.py:1778-1856): 16-channel tiles of a slot's kept channels
+// down (progressive.py:1778-1856): 32-channel tiles of a slot's kept channels
 
 struct DownArgs {
   const uint16_t *down;
@@ -1594,68 +1595,72 @@ struct DownArgs {
   int H, I, K, N, F, max_tiles;
 };
 
+constexpr int kDownOutputs = 4;  // outputs per down thread (H / 4 threads)
+
+// Workgroup per (32-channel tile, token). The tile's channel ids and
+// activations are loaded once by its first 32 threads into LDS (the tile
+// stops at the count or at the first invalid id); every thread then issues
+// the tile's 32 row loads together for its four outputs.
 __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
-  const int tile = blockIdx.x, t = blockIdx.y;
+  __shared__ int tile_channel[kDownTile];
+  __shared__ float tile_act[kDownTile];
+  __shared__ uint32_t tile_live;
+  const int tile = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   int k = -1, first = 0, count = 0;
   for (int s = 0; s < a.K; ++s) {
     const int c = a.counts[t * a.K + s];
     const int ts = a.down_tile_starts[t * a.K + s];
-    if (tile >= ts && tile < ts + (c + 15) / 16) {
+    if (tile >= ts && tile < ts + (c + kDownTile - 1) / kDownTile) {
       k = s;
-      first = (tile - ts) * 16;
+      first = (tile - ts) * kDownTile;
       count = c;
     }
   }
   if (k < 0 || tile >= a.max_tiles) return;
-  const int o = threadIdx.x * 8;
-  if (o >= a.H) return;
   const int e = a.ids[t * a.K + k];
   const bool local = is_active(a.padding, t) && e >= 0;
   const int start = a.starts[t * a.K + k];
-  // the tile's 16 kept positions, a prefix of which is valid (the tile stops
-  // at the count or at the first invalid id); every load is issued
-  // unconditionally from a clamped index or a zero source
-  const int32_t *kept = a.next_ids + static_cast<long>(t) * a.F;
-  int logical[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) logical[j] = load_global(kept + min(start + first + j, a.F - 1));
-  uint32_t live = 0;
-  bool ok = true;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    ok = ok && first + j < count && start + first + j < a.F && logical[j] >= 0 &&
-         logical[j] < a.N;
-    live |= ok ? 1u << j : 0u;
+  int logical = 0;
+  if (tid < kDownTile) {
+    const int j = first + tid;
+    logical = load_global(a.next_ids + static_cast<long>(t) * a.F + min(start + j, a.F - 1));
+    const bool live = j < count && start + j < a.F && logical >= 0 && logical < a.N;
+    // the tile's valid ids: the prefix before the first invalid one
+    const uint64_t invalid = __ballot(!live) | ~((1ull << kDownTile) - 1ull);
+    if (tid == 0) tile_live = static_cast<uint32_t>((1ull << __builtin_ctzll(invalid)) - 1ull);
+    tile_channel[tid] = live ? logical % a.I : 0;
   }
-  const uint16_t *acts = a.activations + static_cast<long>(t) * a.N;
-  const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + o;
-  float act[16];
-  uint4 w[16];
+  __syncthreads();
+  const uint32_t live = tile_live;
+  const int o = tid * kDownOutputs;
+  const bool outputs = o < a.H;
+  const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + min(o, a.H - 4);
+  uint2 w[kDownTile];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    const bool use = (live >> j) & 1u;
-    act[j] = bf16f(load_global(acts + (use ? logical[j] : 0)));
-    const uint4 *source = (use && local) ? reinterpret_cast<const uint4 *>(
-                                               rows + static_cast<long>(logical[j] % a.I) * a.H)
-                                         : &kZeroVector;
-    w[j] = load_global(source);
+  for (int j = 0; j < kDownTile; ++j) {
+    const bool use = outputs && local && ((live >> j) & 1u);
+    w[j] = load_global(use ? reinterpret_cast<const uint2 *>(rows + static_cast<long>(tile_channel[j]) * a.H)
+                           : reinterpret_cast<const uint2 *>(&kZeroVector));
   }
-  float acc[8];
+  if (tid < kDownTile)
+    tile_act[tid] =
+        (live >> tid) & 1u ? bf16f(load_global(a.activations + static_cast<long>(t) * a.N + logical)) : 0.0f;
+  __syncthreads();
+  if (!outputs) return;
+  float acc[kDownOutputs];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  for (int i = 0; i < kDownOutputs; ++i) acc[i] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < kDownTile; ++j) {
     if (!((live >> j) & 1u)) break;
-    const uint32_t wv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc[2 * i] = fmaf(__uint_as_float(wv[i] << 16), act[j], acc[2 * i]);
-      acc[2 * i + 1] = fmaf(__uint_as_float(wv[i] & 0xffff0000u), act[j], acc[2 * i + 1]);
-    }
+    const float act = tile_act[j];
+    acc[0] = fmaf(__uint_as_float(w[j].x << 16), act, acc[0]);
+    acc[1] = fmaf(__uint_as_float(w[j].x & 0xffff0000u), act, acc[1]);
+    acc[2] = fmaf(__uint_as_float(w[j].y << 16), act, acc[2]);
+    acc[3] = fmaf(__uint_as_float(w[j].y & 0xffff0000u), act, acc[3]);
   }
   float *out = a.parts + (static_cast<long>(t) * a.max_tiles + tile) * a.H + o;
   *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  *reinterpret_cast<float4 *>(out + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
 }
 
 // ---------------------------------------------------------------------------
@@ -1683,7 +1688,7 @@ constexpr int kTileBatch = 8;        // tile partials loaded together per thread
 // Workgroup = `columns` outputs of one token, 512 threads (64 outputs below
 // 16 tokens for latency, 256 from there: every workgroup folds its token's
 // encoder tiles, so fewer, wider workgroups read them fewer times). Thread
-// item (slot k, output) sums the slot's 16-channel tile partials in tile order
+// item (slot k, output) sums the slot's 32-channel tile partials in tile order
 // (all loads of a batch issued together) and rounds to BF16; one thread per
 // output then mixes the slots in order with the router weights and adds the
 // decoder correction. The per-(slot, output) values live in dynamic LDS.
@@ -1715,7 +1720,7 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
     const int k = item / columns, column = item % columns;
     const int o = o0 + column;
     const int first = a.down_tile_starts[t * K + k];
-    const int tiles = min((a.counts[t * K + k] + 15) / 16, a.max_tiles - first);
+    const int tiles = min((a.counts[t * K + k] + kDownTile - 1) / kDownTile, a.max_tiles - first);
     const float *parts = a.down_parts + (static_cast<long>(t) * a.max_tiles + first) * a.H +
                          min(o, a.H - 1);
     float total = 0.0f;
@@ -1858,7 +1863,7 @@ Shape shape_of(const cfmoe_dims *d) {
   s.keep = d->keep;
   s.splits = s.B < 8 ? s.B : 8;
   s.span = (s.B + s.splits - 1) / s.splits;
-  s.max_tiles = (s.F + 15) / 16 + s.K - 1;
+  s.max_tiles = (s.F + kDownTile - 1) / kDownTile + s.K - 1;
   s.encoder_tiles = (s.I + 63) / 64;
   s.screened = s.F < s.N;
   return s;
@@ -2259,7 +2264,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   dn.N = s.N;
   dn.F = s.F;
   dn.max_tiles = s.max_tiles;
-  const int down_threads = ((s.H / 8 + kWave - 1) / kWave) * kWave;
+  const int down_threads = ((s.H / kDownOutputs + kWave - 1) / kWave) * kWave;
   if (stages & (1u << CFMOE_STAGE_DOWN)) {
     hipLaunchKernelGGL(down_kernel, dim3(s.max_tiles, tokens), dim3(down_threads), 0, stream,
                        dn);

@@ -118,8 +118,8 @@ typedef struct cfmoe_workspace {
   int32_t *starts;            /* [cap, K] */
   int32_t *counts;            /* [cap, K] */
   int32_t *tile_starts;       /* [cap, K] 128-channel tiles */
-  int32_t *down_tile_starts;  /* [cap, K] 16-channel tiles */
-  float *down_parts;          /* [cap, F/16 + K, H] */
+  int32_t *down_tile_starts;  /* [cap, K] 32-channel tiles */
+  float *down_parts;          /* [cap, ceil(F/32) + K - 1, H] */
   float *encoder_parts;       /* [cap, K, ceil(I/64), R] */
   float *latent;              /* [cap, R] */
   int32_t *group_experts;     /* [cap * K] expert of each tile of <= 16 pairs, ascending */

@@ -36,7 +36,7 @@
  *    1 / (1 + exp(-x)) with IEEE division.
  *  - Exact dot of a native row: 64 lane partials (lane l takes coordinates
  *    512 j + 8 l + i in (j, i) order) then a pairwise tree over lane ids.
- *  - Down: each slot's selected channels in ascending order, in tiles of 16;
+ *  - Down: each slot's selected channels in ascending order, in tiles of 32;
  *    fma chain per tile, tiles summed in order, BF16 per slot.
  *  - Encode: skipped channels in 64-channel tiles; fma chain per tile; tiles
  *    summed in order; BF16 per slot; latent = fma chain over slots.
@@ -537,6 +537,8 @@ void orc_exact(int T, int H, int I, int K, int F, const uint16_t *gate_up,
 /* ------------------------------------------------------------------ */
 /* down: progressive.py:1778-1856; values [T, K, H] (BF16-rounded sums)  */
 
+#define DOWN_TILE 32 /* selected channels per tile (the reference tiles 128) */
+
 void orc_down(int T, int H, int I, int K, int F, const uint16_t *down,
               const uint16_t *activations, const int32_t *ids, const uint8_t *padding,
               const int32_t *next_ids, const int32_t *counts, const int32_t *starts,
@@ -550,9 +552,9 @@ void orc_down(int T, int H, int I, int K, int F, const uint16_t *down,
       int e = ids[t * K + k];
       int count = counts[t * K + k], start = starts[t * K + k];
       for (int o = 0; o < H; ++o) total[o] = 0.0f;
-      for (int begin = 0; begin < count; begin += 16) {
+      for (int begin = 0; begin < count; begin += DOWN_TILE) {
         for (int o = 0; o < H; ++o) tile[o] = 0.0f;
-        for (int j = begin; j < begin + 16 && j < count; ++j) {
+        for (int j = begin; j < begin + DOWN_TILE && j < count; ++j) {
           int logical = next_ids[(long)t * F + start + j];
           int c = logical % I;
           float a = bf16_to_float(activations[(long)t * N + logical]);
