@@ -1106,15 +1106,17 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int packed = block_exclusive(above_here | (tied_here << 16), scratch, &packed_total);
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
   int above_before = packed & 0xffff, tied_before = packed >> 16;
-  // the next slot start at or after this thread's first candidate
-  int next_slot = (first + a.I - 1) / a.I, boundary = next_slot * a.I;
+  // the slot of the current candidate and the next slot start at or after
+  // this thread's first candidate (no division per key)
+  int slot = first / a.I, next_slot = (first + a.I - 1) / a.I, boundary = next_slot * a.I;
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) {
     if (!valid(j)) continue;
     const int i = first + j;
     // the first candidate of a slot: the kept ids before it start the slot
     if (i == boundary) {
-      slot_start[next_slot++] = any ? min(above_before + min(tied_before, room), a.F) : 0;
+      slot_start[next_slot] = any ? min(above_before + min(tied_before, room), a.F) : 0;
+      slot = next_slot++;
       boundary += a.I;
     }
     bool keep = false;
@@ -1130,11 +1132,10 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
       if (key[j] > cutoff) ++above_before;
       if (position < a.F) {
         a.next_ids[static_cast<long>(t) * a.F + position] = i;
-        const int k = i / a.I;
         // the channel's bit for this pair in its tile's mask (OR: any order)
-        const int slot_tile = a.tile_masks ? slot_tiles[k] : -1;
+        const int slot_tile = a.tile_masks ? slot_tiles[slot] : -1;
         if (slot_tile >= 0)
-          atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - k * a.I)],
+          atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
                    1u << (slot_tile % kGroupPairs));
       }
     }
