@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 POINT = 1
 GELU = 2
@@ -92,6 +92,7 @@ WORKSPACE_FIELDS = (
     ("group_total", "int32"),
     ("pair_tiles", "int32"),
     ("tile_masks", "int32"),
+    ("down_order", "int32"),
 )
 
 

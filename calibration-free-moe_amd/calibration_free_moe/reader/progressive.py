@@ -214,6 +214,8 @@ class ReaderWorkspace:
         self.group_total = buffer("group_total", (1,))
         self.pair_tiles = buffer("pair_tiles", (capacity * k,))
         self.tile_masks = buffer("tile_masks", (capacity * n,))
+        # Down workgroups' items grouped by expert per XCD, and their builders' records.
+        self.down_order = buffer("down_order", (self._sizes["down_order"] // 4,))
         # The reference's last-arrival counters; these kernels need none but the
         # attributes stay (all zero) for callers that inspect them.
         self.screen_counters = torch.zeros(
@@ -245,7 +247,7 @@ class ReaderWorkspace:
             *self.scores, self.starts, self.counts, self.tile_starts,
             self.down_tile_starts, self.down_parts, self.encoder_parts, self.latent,
             self.group_experts, self.group_starts, self.group_counts, self.group_pairs,
-            self.group_total, self.pair_tiles, self.tile_masks,
+            self.group_total, self.pair_tiles, self.tile_masks, self.down_order,
         )
         self.bytes = sum(t.numel() * t.element_size() for t in buffers)
         self.charged = False
@@ -291,6 +293,7 @@ _WORKSPACE_ATTRS = (
     ("group_total", "group_total"),
     ("pair_tiles", "pair_tiles"),
     ("tile_masks", "tile_masks"),
+    ("down_order", "down_order"),
 )
 
 

@@ -309,7 +309,7 @@ struct PrepareArgs {
 };
 
 constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
-constexpr int kWorkspaceBuffers = 31;  // cfmoe_workspace pointers after capacity
+constexpr int kWorkspaceBuffers = 32;  // cfmoe_workspace pointers after capacity
 constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
@@ -1449,9 +1449,102 @@ struct GroupExactArgs {
   const uint16_t *encoder_t;
   float *parts;  // encoder partials
   int tiles, encode_items;
+  // the down kernel's workgroup order, built by the first kDownBuilders
+  // workgroups (or NULL): list of down_blocks items, then per-builder slot
+  // records (two words each) from word order_words, slot_capacity per builder
+  int32_t *down_order;
+  const int32_t *pair_tiles;
+  const int32_t *down_tile_starts;
+  int max_tiles, down_blocks, order_words, slot_capacity;
 };
 
 constexpr int kMaxHidden = 2048;
+constexpr int kDownBuilders = 8;  // one per XCD
+
+// Builder x of the down kernel's workgroup order. Workgroup b of the down
+// launch runs on XCD b % 8, in the order b / 8 there; entry 8 r + x of the
+// list gives XCD x the r-th item of its run, and the runs split the items,
+// in expert order (the routing's tiles of pairs, each pair's tiles in turn,
+// then the pairs outside the tiles), into eight contiguous parts: a tile's
+// pairs then read their expert's down rows close together on one XCD, whose
+// L2 serves the rows they share. Entries past a run hold -1. Every builder
+// derives the whole order from the workspace (no communication between
+// workgroups); loads are issued four chunks at a time.
+__device__ void build_down_order(const GroupExactArgs &a, int x) {
+  const int lane = threadIdx.x & 63;
+  const int pairs = a.T * a.K;
+  const int slots = kGroupPairs * load_global(a.group_total);
+  uint2 *records = reinterpret_cast<uint2 *>(a.down_order + a.order_words) +
+                   static_cast<long>(x) * a.slot_capacity;
+  // every pair's tile count; grouped pairs leave (tiles, first item) at their slot
+  int total = 0;
+  for (int i0 = 0; i0 < pairs; i0 += 4 * kWave) {
+    int slot[4], count[4], first[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(i0 + kWave * u + lane, pairs - 1);
+      slot[u] = load_global(a.pair_tiles + i);
+      count[u] = load_global(a.counts + i);
+      first[u] = load_global(a.down_tile_starts + i);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + kWave * u + lane;
+      if (i >= pairs) continue;
+      const int tiles = (count[u] + kDownTile - 1) / kDownTile;
+      total += tiles;
+      if (slot[u] >= 0)
+        records[slot[u]] = make_uint2(tiles, static_cast<uint32_t>((i / a.K) * a.max_tiles + first[u]));
+    }
+  }
+  total = wave_sum_all(total);
+  __syncthreads();  // the slot records are visible to every lane
+  const int run = (total + 7) / 8, lo = x * run, hi = min(total, lo + run);
+  int placed = 0;
+  // the lane's n items item0 + j follow the lower lanes' and those placed
+  auto place = [&](int n, int item0) {
+    const int inclusive = wave_inclusive(n);
+    int m = placed + inclusive - n;
+    for (int j = 0; j < n; ++j, ++m)
+      if (m >= lo && m < hi) a.down_order[8 * (m - lo) + x] = item0 + j;
+    placed += __builtin_amdgcn_readlane(inclusive, 63);
+  };
+  for (int s0 = 0; s0 < slots; s0 += 4 * kWave) {
+    uint2 record[4];
+    int members[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = min(s0 + kWave * u + lane, slots - 1);
+      record[u] = load_global(records + s);
+      members[u] = load_global(a.group_counts + s / kGroupPairs);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = s0 + kWave * u + lane;
+      const bool valid = s < slots && s % kGroupPairs < members[u];
+      place(valid ? static_cast<int>(record[u].x) : 0, static_cast<int>(record[u].y));
+    }
+  }
+  for (int i0 = 0; i0 < pairs; i0 += 4 * kWave) {
+    int slot[4], count[4], first[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = min(i0 + kWave * u + lane, pairs - 1);
+      slot[u] = load_global(a.pair_tiles + i);
+      count[u] = load_global(a.counts + i);
+      first[u] = load_global(a.down_tile_starts + i);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + kWave * u + lane;
+      const bool outside = i < pairs && slot[u] < 0;
+      place(outside ? (count[u] + kDownTile - 1) / kDownTile : 0,
+            (min(i, pairs - 1) / a.K) * a.max_tiles + first[u]);
+    }
+  }
+  // the rest of this XCD's run is empty
+  for (int r = max(hi - lo, 0) + lane; r < a.down_blocks / 8; r += kWave) a.down_order[8 * r + x] = -1;
+}
 
 __device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, int logical,
                                               float g, float u) {
@@ -1471,8 +1564,17 @@ constexpr int kGroupExactWaves = 1;
 __global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(8))) void
 group_exact_kernel(GroupExactArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  if (static_cast<int>(blockIdx.x) >= a.tile_items) {
-    const int item = blockIdx.x - a.tile_items;
+  // the first kDownBuilders workgroups (dispatched first) build the down order
+  int block = blockIdx.x;
+  if (a.down_order) {
+    if (block < kDownBuilders) {
+      build_down_order(a, block);
+      return;
+    }
+    block -= kDownBuilders;
+  }
+  if (block >= a.tile_items) {
+    const int item = block - a.tile_items;
     if (item < a.encode_items) {
       // recovery encoder item (tile, slot, token), tile fastest; it reads no
       // exact result (a skipped channel is never completed)
@@ -1494,9 +1596,8 @@ group_exact_kernel(GroupExactArgs a) {
     }
     return;
   }
-  const int z = blockIdx.x / a.channel_groups;
-  const int c =
-      __builtin_amdgcn_readfirstlane((blockIdx.x % a.channel_groups) * kGroupExactWaves + wave);
+  const int z = block / a.channel_groups;
+  const int c = __builtin_amdgcn_readfirstlane((block % a.channel_groups) * kGroupExactWaves + wave);
   if (c >= a.I) return;
   // The tile count, the tile's expert, pair count and 16 pair slots and this
   // channel's mask, through the scalar cache in one round trip: z < tile bound
@@ -1592,6 +1693,7 @@ struct DownArgs {
   const int32_t *counts;
   const int32_t *starts;
   const int32_t *down_tile_starts;
+  const int32_t *order;  // workgroup b's item t * max_tiles + tile (-1: none), or NULL
   float *parts;
   int H, I, K, N, F, max_tiles;
 };
@@ -1606,7 +1708,14 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   __shared__ int tile_channel[kDownTile];
   __shared__ float tile_act[kDownTile];
   __shared__ uint32_t tile_live;
-  const int tile = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  int tile = blockIdx.x, t = blockIdx.y;
+  const int tid = threadIdx.x;
+  if (a.order) {
+    const int item = load_uniform(a.order + blockIdx.x);
+    if (item < 0) return;
+    tile = item % a.max_tiles;
+    t = item / a.max_tiles;
+  }
   int k = -1, first = 0, count = 0;
   for (int s = 0; s < a.K; ++s) {
     const int c = a.counts[t * a.K + s];
@@ -1870,6 +1979,19 @@ Shape shape_of(const cfmoe_dims *d) {
   return s;
 }
 
+// down_order layout: the down kernel's workgroup list (capacity * max_tiles + 8
+// entries, rounded up to even), then kDownBuilders areas of slot records,
+// 16 * capacity * K records of two words each (a slot per routing-tile pair:
+// tiles <= T * K).
+long down_list_words(long capacity, const Shape &s) {
+  return (capacity * s.max_tiles + 8 + 1) / 2 * 2;
+}
+long down_slot_capacity(long capacity, const Shape &s) { return kGroupPairs * capacity * s.K; }
+long down_order_words(long capacity, const Shape &s) {
+  return down_list_words(capacity, s) + 2L * kDownBuilders * down_slot_capacity(capacity, s);
+}
+
+
 int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
                    const cfmoe_workspace *ws, const void *hidden, const void *router_ids,
                    const void *router_weights, const uint8_t *padding, int tokens,
@@ -1963,6 +2085,7 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
       4,                                      // group_total
       cap * s.K * 4,                          // pair_tiles
       cap * n * 4,                            // tile_masks (tiles * I <= cap * N)
+      down_order_words(cap, s) * 4,           // down_order (list + builders' slot records)
   };
   const int written = count < kWorkspaceBuffers ? count : kWorkspaceBuffers;
   for (int i = 0; i < written; ++i) sizes[i] = table[i];
@@ -2173,6 +2296,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   // needs no LDS (R = kDirectRank; the LDS encoder's dynamic LDS would apply to
   // every exact workgroup and halve their occupancy)
   const bool small = tokens < kGroupExactTokens;
+  // grouped batches: the exact stage builds the down kernel's workgroup order
+  // (expert-grouped per XCD) and the down stage reads it
+  const bool down_order = !small;
+  const int down_blocks = (tokens * s.max_tiles + 7) / 8 * 8;
   const bool encode_in_exact = s.R > 0 && (small || s.R == kDirectRank);
   const bool fuse_encode = encode_in_exact && small && (stages & (1u << CFMOE_STAGE_EXACT));
   const bool fuse_direct = encode_in_exact && !small && (stages & (1u << CFMOE_STAGE_EXACT));
@@ -2229,7 +2356,15 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       gx.parts = en.parts;
       gx.tiles = en.tiles;
       gx.encode_items = fuse_direct ? s.encoder_tiles * s.K * tokens : 0;
-      hipLaunchKernelGGL(group_exact_kernel, dim3(gx.tile_items + gx.encode_items + tokens),
+      gx.down_order = workspace->down_order;
+      gx.pair_tiles = workspace->pair_tiles;
+      gx.down_tile_starts = workspace->down_tile_starts;
+      gx.max_tiles = s.max_tiles;
+      gx.down_blocks = down_blocks;
+      gx.order_words = static_cast<int>(down_list_words(workspace->capacity, s));
+      gx.slot_capacity = static_cast<int>(down_slot_capacity(workspace->capacity, s));
+      hipLaunchKernelGGL(group_exact_kernel,
+                         dim3(kDownBuilders + gx.tile_items + gx.encode_items + tokens),
                          dim3(64 * kGroupExactWaves), 0, stream, gx);
     } else {
       ex.encode = en;
@@ -2258,6 +2393,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   dn.counts = workspace->counts;
   dn.starts = workspace->starts;
   dn.down_tile_starts = workspace->down_tile_starts;
+  dn.order = down_order ? workspace->down_order : nullptr;
   dn.parts = workspace->down_parts;
   dn.H = s.H;
   dn.I = s.I;
@@ -2267,8 +2403,11 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   dn.max_tiles = s.max_tiles;
   const int down_threads = ((s.H / kDownOutputs + kWave - 1) / kWave) * kWave;
   if (stages & (1u << CFMOE_STAGE_DOWN)) {
-    hipLaunchKernelGGL(down_kernel, dim3(s.max_tiles, tokens), dim3(down_threads), 0, stream,
-                       dn);
+    if (down_order)
+      hipLaunchKernelGGL(down_kernel, dim3(down_blocks), dim3(down_threads), 0, stream, dn);
+    else
+      hipLaunchKernelGGL(down_kernel, dim3(s.max_tiles, tokens), dim3(down_threads), 0, stream,
+                         dn);
     if ((rc = check_launch("down"))) return rc;
   }
   if (!(stages & (1u << CFMOE_STAGE_OUTPUT))) return 0;

@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 4
+#define CFMOE_ABI_VERSION 5
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -129,11 +129,13 @@ typedef struct cfmoe_workspace {
   int32_t *group_total;       /* [1] number of tiles */
   int32_t *pair_tiles;        /* [cap * K] slot 16 z + p of each pair in group_pairs, or -1 */
   uint32_t *tile_masks;       /* [cap * N] per (tile, channel): bit p set if pair p kept it */
+  int32_t *down_order;        /* down workgroups' items grouped by expert per XCD, then the
+                                 builders' slot records (size from cfmoe_workspace_sizes) */
   double *read_work;          /* [20] read statistics (progressive.py:3507-3515) */
 } cfmoe_workspace;
 
 /* Byte sizes of every workspace buffer, in struct order after `capacity`
- * (31 entries, read_work excluded). Returns the number written. */
+ * (32 entries, read_work excluded). Returns the number written. */
 CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
                           int32_t count);
 
