@@ -207,6 +207,30 @@ def test_hot_expert_splits_into_screen_tiles():
         assert np.array_equal(masks[z], want)
         seen += members
     assert sorted(seen) == list(range(tokens * top_k))
+    # the down kernel's workgroup list: every (token, tile) item once, in the
+    # routing's expert order (tiles' pairs, each pair's tiles, then the pairs
+    # outside the tiles) cut into eight contiguous runs; entry 8 r + x holds
+    # run x's r-th item and the entries past a run hold -1
+    max_tiles = ws.down_tiles
+    kept = ws.counts[:tokens].cpu().numpy()
+    first_tile = ws.down_tile_starts[:tokens].cpu().numpy()
+    sequence = []
+    def items(p):
+        t, k = divmod(p, top_k)
+        return [t * max_tiles + int(first_tile[t, k]) + j for j in range(-(-int(kept[t, k]) // 32))]
+    for first, count in zip(starts, counts):
+        for p in pairs[first:first + count]:
+            sequence += items(p)
+    for p in range(tokens * top_k):
+        if pair_tiles[p] < 0:
+            sequence += items(p)
+    blocks = -(-tokens * max_tiles // 8) * 8
+    order = ws.down_order[:blocks].cpu().numpy().reshape(-1, 8)
+    run = -(-len(sequence) // 8)
+    for x in range(8):
+        want = sequence[x * run:(x + 1) * run]
+        assert order[: len(want), x].tolist() == want
+        assert (order[len(want):, x] == -1).all()
 
 
 @pytest.mark.parametrize("score,rank,width", [("point", 16, 256), ("recovery-aware", 16, 256),
