@@ -47,8 +47,15 @@ CONFIGS = {
     "c1": (2048, 1024, 64, 8, 1, 1, 0.123, 0.625, "OLMoE-1B-7B layer, batch 1"),
     "c2": (2048, 1024, 64, 8, 16, 64, 0.123, 0.625, "OLMoE-1B-7B layer x16, batch 64"),
     "c3": (2048, 768, 128, 8, 48, 1, 0.123, 0.625, "Qwen3-30B-A3B layer x48"),
-    "c5": (2048, 512, 256, 8, 16, 1, 0.123, 0.625, "256-expert I=512 layer x16"),
+    "c4": (2048, 768, 128, 8, 48, 256, 0.123, 0.625,
+           "Qwen3-30B-A3B layer x48, Zipf(1.2) expert popularity"),
+    "c5": (2048, 512, 256, 8, 16, 1, 0.123, 0.625,
+           "256-expert I=512 layer x16, dense I=512 shared expert beside it"),
 }
+# c4 routes the c3 layers' weights with skewed popularity (same weight seeds)
+WEIGHT_SEEDS = {"c1": 1, "c2": 2, "c3": 3, "c4": 3, "c5": 5}
+ZIPF = {"c4": 1.2}
+SHARED_WIDTH = {"c5": 512}
 
 
 def log(message: str) -> None:
@@ -76,17 +83,34 @@ def device_weights(hidden, width, experts, rank, seed, device, std=0.02):
     }
 
 
-def device_inputs(weights, tokens, top_k, seed, device):
-    """A routed decode batch: N(0, 1) states with 1 % of dims x20, softmax top-k."""
+def device_inputs(weights, tokens, top_k, seed, device, zipf=None):
+    """A routed decode batch: N(0, 1) states with 1 % of dims x20, softmax top-k.
+
+    With `zipf` = s the experts are drawn instead with popularity p_e
+    proportional to rank^-s (a seeded permutation of the experts): top-k
+    without replacement by Gumbel-top-k on log p_e, weights the renormalised
+    softmax of the chosen perturbed scores (recipe of tests/synthetic.py).
+    """
     hidden = weights["router"].shape[1]
+    experts = weights["router"].shape[0]
     g = torch.Generator(device=device).manual_seed(seed)
     x = torch.randn(tokens, hidden, generator=g, device=device)
     dims = torch.randperm(hidden, generator=g, device=device)[: max(1, round(0.01 * hidden))]
     x[:, dims] *= 20
     x = x.bfloat16()
-    logits = (x.float() @ weights["router"].float().T).bfloat16().float()
-    probabilities, ids = torch.softmax(logits, -1).topk(top_k, -1)
-    probabilities = (probabilities / probabilities.sum(-1, keepdim=True)).float().contiguous()
+    if zipf is None:
+        logits = (x.float() @ weights["router"].float().T).bfloat16().float()
+        probabilities, ids = torch.softmax(logits, -1).topk(top_k, -1)
+        probabilities = (probabilities / probabilities.sum(-1, keepdim=True)).float().contiguous()
+    else:
+        rank = torch.arange(1, experts + 1, dtype=torch.float64, device=device)
+        popularity = rank.pow(-zipf)
+        permutation = torch.randperm(experts, generator=g, device=device)
+        log_p = torch.log(popularity / popularity.sum())[permutation]
+        uniform = torch.rand(tokens, experts, generator=g, device=device, dtype=torch.float64)
+        scores = log_p[None, :] - torch.log(-torch.log(uniform))
+        ids = scores.topk(top_k, dim=-1).indices
+        probabilities = torch.softmax(scores.gather(1, ids), dim=-1).float().contiguous()
     return {"hidden": x, "ids": ids.to(torch.int64).contiguous(), "weights": probabilities,
             "out": torch.empty_like(x)}
 
@@ -243,32 +267,69 @@ def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> tuple[fl
     return elapsed * 1e3 / steps, [b.elapsed_time(e) for b, e in events]
 
 
-_WEIGHT_CACHE: dict[str, list] = {}
+_WEIGHT_CACHE: dict[int, list] = {}
 
 
 def layer_weights(name: str, layers: int, device) -> list:
     h, i, e, k, _, _, _, _, _ = CONFIGS[name]
-    cached = _WEIGHT_CACHE.get(name)
+    base = WEIGHT_SEEDS[name]
+    cached = _WEIGHT_CACHE.get(base)
     if cached is None or len(cached) != layers:
         _WEIGHT_CACHE.clear()
         torch.cuda.empty_cache()
         started = time.perf_counter()
-        cached = [device_weights(h, i, e, 32, seed=1000 * int(name[1:]) + layer, device=device)
+        cached = [device_weights(h, i, e, 32, seed=1000 * base + layer, device=device)
                   for layer in range(layers)]
         torch.cuda.synchronize()
         log(f"[{name}] generated {layers} layers in {time.perf_counter() - started:.1f}s")
-        _WEIGHT_CACHE[name] = cached
+        _WEIGHT_CACHE[base] = cached
     return cached
+
+
+def shared_expert_us(name: str, stack: list, args, device) -> float | None:
+    """Dense always-on shared expert beside the reader (C5), timed on its own.
+
+    One BF16 SwiGLU MLP of width SHARED_WIDTH per layer on the same decode
+    batch: gate/up [2W, H] and down [H, W] N(0, 0.02^2), computed dense with
+    library GEMMs (hipBLASLt); its time is reported separately from the
+    reader's, as the configuration asks.
+    """
+    width = SHARED_WIDTH.get(name)
+    if width is None:
+        return None
+    h = CONFIGS[name][0]
+    g = torch.Generator(device=device).manual_seed(5000)
+    mlps = [((torch.randn(2 * width, h, generator=g, device=device) * 0.02).bfloat16(),
+             (torch.randn(h, width, generator=g, device=device) * 0.02).bfloat16())
+            for _ in stack]
+    outs = [torch.empty_like(d["hidden"]) for _, d in stack]
+
+    def run():
+        for (gate_up, down), (_, d), out in zip(mlps, stack, outs):
+            gu = d["hidden"] @ gate_up.T
+            act = torch.nn.functional.silu(gu[:, :width]) * gu[:, width:]
+            torch.matmul(act, down.T, out=out)
+
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    ms, _ = time_graph(graph, args.warmup, args.steps)
+    return ms * 1e3 / len(stack)
 
 
 def run_config(name: str, args, device) -> dict:
     h, i, e, k, layers, tokens, retention, keep, description = CONFIGS[name]
     layers = args.layers or layers
     tokens = args.tokens or tokens
+    retention = getattr(args, "retention", 0.0) or retention
+    keep = getattr(args, "keep", 0.0) or keep
     rank = 32
     plan = compile_budget(hidden_size=h, expert_width=i, top_k=k, retention=retention,
                           screen_keep=keep)
-    log(f"[{name}] {layers} layers (H={h} I={i} E={e} K={k}) batch {tokens}")
+    log(f"[{name}] {layers} layers (H={h} I={i} E={e} K={k}) batch {tokens} "
+        f"retention {retention} keep {keep}")
     weights = layer_weights(name, layers, device)
     workspace = ReaderWorkspace(plan, e, rank, tokens, device)
     stack = []
@@ -277,7 +338,8 @@ def run_config(name: str, args, device) -> dict:
             w["gate_up"], w["down"], w["encoder"], w["decoder"], plan, tokens,
             sketch=w["sketch"], selection_score="point", workspace=workspace,
         )
-        stack.append((reader, device_inputs(w, tokens, k, seed=7919 * layer + tokens, device=device)))
+        stack.append((reader, device_inputs(w, tokens, k, seed=7919 * layer + tokens, device=device,
+                                            zipf=ZIPF.get(name))))
     torch.cuda.synchronize()
     for reader, d in stack:
         reader(d["hidden"], d["ids"], d["weights"], out=d["out"])
@@ -318,6 +380,7 @@ def run_config(name: str, args, device) -> dict:
         end.record()
         torch.cuda.synchronize()
         stage_us[stage] = begin.elapsed_time(end) * 1e3 / (repeats * layers)
+    shared_us = shared_expert_us(name, stack, args, device)
     dominant = max(STAGE_BYTES, key=lambda s: stage_us[s])
     dominant_bytes = sum(mean_bytes[key] for key in stage_bytes(dominant, tokens, rank))
     achieved = dominant_bytes / (stage_us[dominant] * 1e-6) / 1e9
@@ -326,6 +389,10 @@ def run_config(name: str, args, device) -> dict:
         "description": description,
         "layers": layers,
         "tokens": tokens,
+        "retention": retention,
+        "screen_keep": keep,
+        "zipf": ZIPF.get(name),
+        "shared_expert_us_per_layer": shared_us,
         "final_count": plan.final_count,
         "ms_per_step": ms_per_step,
         "us_per_layer": us_per_layer,
@@ -482,8 +549,11 @@ def main() -> int:
     parser.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     parser.add_argument("--layers", type=int, default=0)
     parser.add_argument("--tokens", type=int, default=0)
-    parser.add_argument("--extra", default="c3:1,c3:128",
-                        help="comma list of config:tokens measured beside the headline")
+    parser.add_argument("--extra",
+                        default="c3:1,c3:32,c3:128,c4:256,c4:256:0.06,c4:256:0.25,"
+                                "c5:1,c5:128,c5:1:0.123:1.0,c5:128:0.123:1.0",
+                        help="comma list of config:tokens[:retention[:screen_keep]] "
+                             "measured beside the headline")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     args = parser.parse_args()
     if args.gpus != 1:
@@ -498,10 +568,12 @@ def main() -> int:
     headline = run_config(args.config, args, device)
     extras = []
     for item in filter(None, args.extra.split(",")):
-        name, _, count = item.partition(":")
+        name, *fields = item.split(":")
         sub = argparse.Namespace(**vars(args))
         sub.layers = 0
-        sub.tokens = int(count) if count else 0
+        sub.tokens = int(fields[0]) if fields and fields[0] else 0
+        sub.retention = float(fields[1]) if len(fields) > 1 else 0.0
+        sub.keep = float(fields[2]) if len(fields) > 2 else 0.0
         torch.cuda.empty_cache()
         extras.append(run_config(name, sub, device))
     probe = stream_probe(device)
@@ -550,9 +622,10 @@ def main() -> int:
         "cpu_baseline": baseline,
         "extra": [
             {key: (round(v, 3) if isinstance(v, float) else v) for key, v in x.items()
-             if key in ("name", "description", "layers", "tokens", "us_per_layer",
-                        "tokens_per_s", "achieved_gbps", "layer_roofline_frac", "dominant",
-                        "dominant_gbps", "stage_us")}
+             if key in ("name", "description", "layers", "tokens", "retention", "screen_keep",
+                        "zipf", "final_count", "us_per_layer", "tokens_per_s", "achieved_gbps",
+                        "layer_roofline_frac", "dominant", "dominant_gbps", "stage_us",
+                        "shared_expert_us_per_layer")}
             for x in extras
         ],
     }

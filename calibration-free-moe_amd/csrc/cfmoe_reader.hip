@@ -314,19 +314,23 @@ constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column blo
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
 
+constexpr int kPrepareWaves = kPrepareThreads / 64;
+
 // LDS of the routing block, carved from the launch's dynamic LDS, which the
 // host sizes for the call's pairs and experts (route_lds_bytes): the pairs'
-// ids in routing order (later the per-expert buckets of pair indices) and
-// sorted per token, then per-expert counters and packed prefixes.
+// ids in routing order (later each pair's rank among the earlier pairs of
+// its expert in its wave's range) and sorted per token, then per-expert
+// counters and packed prefixes, then per-wave per-expert pair counts.
 struct RouteShared {
   int16_t *sorted, *routed;
   int *counts, *base;
+  int16_t *wave_counts;  // [kPrepareWaves][experts]
 };
 
 __host__ __device__ inline long route_pairs_padded(int pairs) { return (pairs + 7) / 8 * 8; }
 
 __host__ __device__ inline long route_lds_bytes(int pairs, int experts) {
-  return 2 * 2 * route_pairs_padded(pairs) + 2 * 4 * (experts + 1);
+  return 2 * 2 * route_pairs_padded(pairs) + 2 * 4 * (experts + 1) + 2 * kPrepareWaves * experts;
 }
 
 __device__ inline RouteShared route_layout(char *lds, int pairs, int experts) {
@@ -336,6 +340,7 @@ __device__ inline RouteShared route_layout(char *lds, int pairs, int experts) {
   r.routed = r.sorted + padded;
   r.counts = reinterpret_cast<int *>(r.routed + padded);
   r.base = r.counts + experts + 1;
+  r.wave_counts = reinterpret_cast<int16_t *>(r.base + experts + 1);
   return r;
 }
 
@@ -425,9 +430,13 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   // Expert-major grouping as a counting sort by expert, stable in pair order:
   // (1) per-expert counts; (2) one scan of packed (members, tiles) gives each
   // expert its member start and first tile z_e, and its tiles are emitted;
-  // (3) pairs drop into per-expert buckets (any order); (4) a pair's final
-  // slot is 16 z_e + its rank by pair index within its bucket.
+  // (3) wave w ranks the pairs of its contiguous range among the earlier
+  // pairs of the same expert (a match of equal experts from one ballot per id
+  // bit, 64 pairs at a time, running per-expert counts of the wave); (4) a
+  // pair's final slot is 16 z_e + its rank within its wave's range + the
+  // counts of the waves before. O(pairs log E), whatever the skew.
   for (int e = tid; e <= a.E; e += kPrepareThreads) counts[e] = 0;
+  for (int i = tid; i < kPrepareWaves * a.E; i += kPrepareThreads) shared.wave_counts[i] = 0;
   __syncthreads();
   for (int p = tid; p < pairs; p += kPrepareThreads) {
     const int e = sorted[p];
@@ -460,26 +469,42 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
     }
     if (tid == kPrepareThreads - 1) base[a.E] = packed_total & 0xffff;
   }
-  __syncthreads();
-  // bucket cursors start at each expert's member start
-  for (int e = tid; e < a.E; e += kPrepareThreads) counts[e] = base[e] & 0xffff;
-  __syncthreads();
-  int16_t *bucket = routed;
-  for (int p = tid; p < pairs; p += kPrepareThreads) {
-    const int e = sorted[p];
-    if (e >= 0) bucket[atomicAdd(&counts[e], 1)] = static_cast<int16_t>(p);
-  }
-  __syncthreads();
-  for (int p = tid; p < pairs; p += kPrepareThreads) {
-    const int e = sorted[p];
-    if (e < 0) continue;
-    const int begin = base[e] & 0xffff, end = base[e + 1] & 0xffff, z = base[e] >> 16;
-    int rank = 0;
-#pragma unroll 8
-    for (int j = begin; j < end; ++j) rank += bucket[j] < p;
-    const int at = kGroupPairs * z + rank;
-    a.group_pairs[at] = p;
-    a.pair_tiles[p] = at;
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    const int chunks = (pairs + 63) / 64;
+    const int per_wave = (chunks + kPrepareWaves - 1) / kPrepareWaves;
+    const int bits = a.E > 1 ? 32 - __builtin_clz(static_cast<unsigned>(a.E - 1)) : 1;
+    int16_t *counted = shared.wave_counts + wave * a.E;
+    int16_t *local_rank = routed;
+    for (int c = wave * per_wave; c < min(chunks, (wave + 1) * per_wave); ++c) {
+      const int p = 64 * c + lane;
+      const int e = p < pairs ? sorted[p] : -1;
+      // lanes holding the same expert: agree on every id bit
+      uint64_t peers = __ballot(e >= 0);
+      for (int b = 0; b < bits; ++b) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t set = __ballot(bit);
+        peers &= bit ? set : ~set;
+      }
+      if (e >= 0) {
+        // every lane of the group reads the running count before its lowest
+        // lane adds the group (LDS operations of a wave complete in order)
+        const int before = counted[e];
+        local_rank[p] = static_cast<int16_t>(before + __popcll(peers & lanes_below(lane)));
+        if (lane == __builtin_ctzll(peers)) counted[e] = static_cast<int16_t>(before + __popcll(peers));
+      }
+    }
+    __syncthreads();
+    for (int p = tid; p < pairs; p += kPrepareThreads) {
+      const int e = sorted[p];
+      if (e < 0) continue;
+      const int owner = (p / 64) / per_wave;
+      int rank = local_rank[p];
+      for (int v = 0; v < owner; ++v) rank += shared.wave_counts[v * a.E + e];
+      const int at = kGroupPairs * (base[e] >> 16) + rank;
+      a.group_pairs[at] = p;
+      a.pair_tiles[p] = at;
+    }
   }
   if (tid == 0) *a.group_total = total_tiles;
   // fixed read charges: one add per slot for all active tokens (integers, exact)
@@ -1561,41 +1586,48 @@ __device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, in
 // kept end at once), can start only when every SIMD of a CU has a free slot.
 constexpr int kGroupExactWaves = 1;
 
-__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(8))) void
-group_exact_kernel(GroupExactArgs a) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  // the first kDownBuilders workgroups (dispatched first) build the down order
+// The grouped exact launch's workgroups that are not (tile, channel) work:
+// the first kDownBuilders build the down order, those past the tile items run
+// recovery encoder items, then one per token writes the zero results of a
+// padded token or of slots with no local expert. Returns the tile item index
+// of a work workgroup, or -1 when the workgroup's part is done.
+__device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, int threads) {
   int block = blockIdx.x;
   if (a.down_order) {
     if (block < kDownBuilders) {
       build_down_order(a, block);
-      return;
+      return -1;
     }
     block -= kDownBuilders;
   }
-  if (block >= a.tile_items) {
-    const int item = block - a.tile_items;
-    if (item < a.encode_items) {
-      // recovery encoder item (tile, slot, token), tile fastest; it reads no
-      // exact result (a skipped channel is never completed)
-      const int tile = item % a.tiles, rest = item / a.tiles;
-      encode_tile_direct(a, tile, rest % a.K, rest / a.K);
-      return;
-    }
-    // zero results of a padded token or of a slot with no local expert
-    const int t = item - a.encode_items;
-    if (t >= a.T) return;
-    const bool active = is_active(a.padding, t);
-    for (int k = 0; k < a.K; ++k) {
-      if (active && a.ids[t * a.K + k] >= 0) continue;
-      const int start = a.starts[t * a.K + k], count = a.counts[t * a.K + k];
-      for (int j = tid; j < count && start + j < a.F; j += 64 * kGroupExactWaves) {
-        const int logical = a.next_ids[static_cast<long>(t) * a.F + start + j];
-        if (logical >= 0 && logical < a.N) exact_results(a, t, logical, 0.0f, 0.0f);
-      }
-    }
-    return;
+  if (block < a.tile_items) return block;
+  const int item = block - a.tile_items;
+  if (item < a.encode_items) {
+    // recovery encoder item (tile, slot, token), tile fastest; it reads no
+    // exact result (a skipped channel is never completed)
+    const int tile = item % a.tiles, rest = item / a.tiles;
+    encode_tile_direct(a, tile, rest % a.K, rest / a.K);
+    return -1;
   }
+  const int t = item - a.encode_items;
+  if (t >= a.T) return -1;
+  const bool active = is_active(a.padding, t);
+  for (int k = 0; k < a.K; ++k) {
+    if (active && a.ids[t * a.K + k] >= 0) continue;
+    const int start = a.starts[t * a.K + k], count = a.counts[t * a.K + k];
+    for (int j = static_cast<int>(threadIdx.x); j < count && start + j < a.F; j += threads) {
+      const int logical = a.next_ids[static_cast<long>(t) * a.F + start + j];
+      if (logical >= 0 && logical < a.N) exact_results(a, t, logical, 0.0f, 0.0f);
+    }
+  }
+  return -1;
+}
+
+__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(8))) void
+group_exact_kernel(GroupExactArgs a) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int block = group_exact_side_items(a, 64 * kGroupExactWaves);
+  if (block < 0) return;
   const int z = block / a.channel_groups;
   const int c = __builtin_amdgcn_readfirstlane((block % a.channel_groups) * kGroupExactWaves + wave);
   if (c >= a.I) return;
@@ -1700,74 +1732,94 @@ struct DownArgs {
 
 constexpr int kDownOutputs = 4;  // outputs per down thread (H / 4 threads)
 
-// Workgroup per (32-channel tile, token). The tile's channel ids and
-// activations are loaded once by its first 32 threads into LDS (the tile
-// stops at the count or at the first invalid id); every thread then issues
-// the tile's 32 row loads together for its four outputs.
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
+
+// Workgroup per (32-channel tile, token), H / 4 threads of four outputs each.
+// Every wave works alone (no LDS, no barrier): the token's slot records
+// (counts, tile starts, ids, starts) come through the scalar cache in one
+// round trip, lanes l < 32 of the wave load the tile's channel id l (the tile
+// stops at the count or at the first invalid id, found by a ballot), the ids
+// are broadcast by lane reads and every thread issues the tile's 32 row loads
+// together, then the 32 activations (one per lane, broadcast the same way).
 __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
-  __shared__ int tile_channel[kDownTile];
-  __shared__ float tile_act[kDownTile];
-  __shared__ uint32_t tile_live;
   int tile = blockIdx.x, t = blockIdx.y;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63;
   if (a.order) {
     const int item = load_uniform(a.order + blockIdx.x);
     if (item < 0) return;
     tile = item % a.max_tiles;
     t = item / a.max_tiles;
   }
-  int k = -1, first = 0, count = 0;
-  for (int s = 0; s < a.K; ++s) {
-    const int c = a.counts[t * a.K + s];
-    const int ts = a.down_tile_starts[t * a.K + s];
-    if (tile >= ts && tile < ts + (c + kDownTile - 1) / kDownTile) {
-      k = s;
-      first = (tile - ts) * kDownTile;
-      count = c;
+  int k = -1, first = 0, count = 0, e = -1, start = 0;
+  if (a.K == 8) {
+    const long row = static_cast<long>(t) * 8;
+    const i32x8 counts = load_uniform(reinterpret_cast<const i32x8 *>(a.counts + row));
+    const i32x8 tiles = load_uniform(reinterpret_cast<const i32x8 *>(a.down_tile_starts + row));
+    const i32x8 ids = load_uniform(reinterpret_cast<const i32x8 *>(a.ids + row));
+    const i32x8 starts = load_uniform(reinterpret_cast<const i32x8 *>(a.starts + row));
+    asm volatile("" ::"s"(counts), "s"(tiles), "s"(ids), "s"(starts));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (tile >= tiles[s] && tile < tiles[s] + (counts[s] + kDownTile - 1) / kDownTile) {
+        k = s;
+        first = (tile - tiles[s]) * kDownTile;
+        count = counts[s];
+        e = ids[s];
+        start = starts[s];
+      }
+    }
+  } else {
+    for (int s = 0; s < a.K; ++s) {
+      const int c = a.counts[t * a.K + s];
+      const int ts = a.down_tile_starts[t * a.K + s];
+      if (tile >= ts && tile < ts + (c + kDownTile - 1) / kDownTile) {
+        k = s;
+        first = (tile - ts) * kDownTile;
+        count = c;
+      }
+    }
+    if (k >= 0) {
+      e = a.ids[t * a.K + k];
+      start = a.starts[t * a.K + k];
     }
   }
   if (k < 0 || tile >= a.max_tiles) return;
-  const int e = a.ids[t * a.K + k];
   const bool local = is_active(a.padding, t) && e >= 0;
-  const int start = a.starts[t * a.K + k];
-  int logical = 0;
-  if (tid < kDownTile) {
-    const int j = first + tid;
-    logical = load_global(a.next_ids + static_cast<long>(t) * a.F + min(start + j, a.F - 1));
-    const bool live = j < count && start + j < a.F && logical >= 0 && logical < a.N;
-    // the tile's valid ids: the prefix before the first invalid one
-    const uint64_t invalid = __ballot(!live) | ~((1ull << kDownTile) - 1ull);
-    if (tid == 0) tile_live = static_cast<uint32_t>((1ull << __builtin_ctzll(invalid)) - 1ull);
-    tile_channel[tid] = live ? logical % a.I : 0;
-  }
-  __syncthreads();
-  const uint32_t live = tile_live;
+  const int j = first + (lane & (kDownTile - 1));
+  const int logical = load_global(a.next_ids + static_cast<long>(t) * a.F + min(start + j, a.F - 1));
+  const bool valid = j < count && start + j < a.F && logical >= 0 && logical < a.N;
+  // the tile's valid ids: the prefix before the first invalid one
+  const uint32_t invalid = static_cast<uint32_t>(__ballot(!valid));
+  const uint32_t live = invalid ? (1u << __builtin_ctz(invalid)) - 1u : 0xffffffffu;
+  const int channel = valid ? logical % a.I : 0;
   const int o = tid * kDownOutputs;
   const bool outputs = o < a.H;
   const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + min(o, a.H - 4);
   uint2 w[kDownTile];
 #pragma unroll
-  for (int j = 0; j < kDownTile; ++j) {
-    const bool use = outputs && local && ((live >> j) & 1u);
-    w[j] = load_global(use ? reinterpret_cast<const uint2 *>(rows + static_cast<long>(tile_channel[j]) * a.H)
-                           : reinterpret_cast<const uint2 *>(&kZeroVector));
+  for (int jj = 0; jj < kDownTile; ++jj) {
+    const int c = __builtin_amdgcn_readlane(channel, jj);
+    const bool use = outputs && local && ((live >> jj) & 1u);
+    w[jj] = load_global(use ? reinterpret_cast<const uint2 *>(rows + static_cast<long>(c) * a.H)
+                            : reinterpret_cast<const uint2 *>(&kZeroVector));
   }
-  if (tid < kDownTile)
-    tile_act[tid] =
-        (live >> tid) & 1u ? bf16f(load_global(a.activations + static_cast<long>(t) * a.N + logical)) : 0.0f;
-  __syncthreads();
+  const bool mine = (live >> (lane & (kDownTile - 1))) & 1u;
+  const uint16_t act_bits =
+      load_global(mine ? a.activations + static_cast<long>(t) * a.N + logical
+                       : reinterpret_cast<const uint16_t *>(&kZeroVector));
+  const int act_lane = static_cast<int>(__float_as_uint(bf16f(act_bits)));
   if (!outputs) return;
   float acc[kDownOutputs];
 #pragma unroll
   for (int i = 0; i < kDownOutputs; ++i) acc[i] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kDownTile; ++j) {
-    if (!((live >> j) & 1u)) break;
-    const float act = tile_act[j];
-    acc[0] = fmaf(__uint_as_float(w[j].x << 16), act, acc[0]);
-    acc[1] = fmaf(__uint_as_float(w[j].x & 0xffff0000u), act, acc[1]);
-    acc[2] = fmaf(__uint_as_float(w[j].y << 16), act, acc[2]);
-    acc[3] = fmaf(__uint_as_float(w[j].y & 0xffff0000u), act, acc[3]);
+  for (int jj = 0; jj < kDownTile; ++jj) {
+    if (!((live >> jj) & 1u)) break;
+    const float act = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(act_lane, jj)));
+    acc[0] = fmaf(__uint_as_float(w[jj].x << 16), act, acc[0]);
+    acc[1] = fmaf(__uint_as_float(w[jj].x & 0xffff0000u), act, acc[1]);
+    acc[2] = fmaf(__uint_as_float(w[jj].y << 16), act, acc[2]);
+    acc[3] = fmaf(__uint_as_float(w[jj].y & 0xffff0000u), act, acc[3]);
   }
   float *out = a.parts + (static_cast<long>(t) * a.max_tiles + tile) * a.H + o;
   *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);

@@ -197,3 +197,32 @@ def forward(w: Weights, x_bits, router_ids, router_weights, *, final_count: int,
         "completed": completed, "values": values, "latent": latent[:, :R],
         "out": out,
     }
+
+
+def forward_parallel(w: Weights, x_bits, router_ids, router_weights, *, padding=None,
+                     workers: int | None = None, **options) -> dict[str, np.ndarray]:
+    """`forward` over contiguous token ranges in threads, results concatenated.
+
+    Every stage of the reader is per token (a token's routing, screen,
+    selection, exact rows, down sums, latent and output read no other token's
+    values), so the ranges' results are the whole call's. ctypes releases the
+    GIL during each C call, so the ranges run on separate cores.
+    """
+    from concurrent.futures import ThreadPoolExecutor
+
+    tokens = x_bits.shape[0]
+    workers = max(1, min(workers or os.cpu_count() or 1, 16, tokens))
+    bounds = np.linspace(0, tokens, workers + 1).astype(int)
+    ranges = [(lo, hi) for lo, hi in zip(bounds[:-1], bounds[1:]) if hi > lo]
+
+    def run(span):
+        lo, hi = span
+        return forward(w, np.ascontiguousarray(x_bits[lo:hi]),
+                       np.ascontiguousarray(router_ids[lo:hi]),
+                       np.ascontiguousarray(router_weights[lo:hi]),
+                       padding=None if padding is None else np.ascontiguousarray(padding[lo:hi]),
+                       **options)
+
+    with ThreadPoolExecutor(len(ranges)) as pool:
+        parts = list(pool.map(run, ranges))
+    return {key: np.concatenate([part[key] for part in parts]) for key in parts[0]}

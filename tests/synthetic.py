@@ -71,7 +71,11 @@ def recovery_bank(down: Tensor, rank: int) -> tuple[Tensor, Tensor]:
     gram = torch.zeros(d.shape[1], d.shape[1], dtype=d.dtype, device=d.device)
     for expert in range(d.shape[0]):
         gram += d[expert] @ d[expert].T
-    _, vectors = torch.linalg.eigh(gram)
+    try:
+        _, vectors = torch.linalg.eigh(gram)
+    except RuntimeError:  # no device eigensolver: solve on the host
+        _, vectors = torch.linalg.eigh(gram.double().cpu())
+        vectors = vectors.to(d.device, d.dtype)
     u = vectors[:, -rank:].flip(-1)
     b = torch.einsum("hr,ehi->eri", u, d)
     return b.to(torch.bfloat16), u.to(torch.bfloat16)

@@ -45,7 +45,8 @@ def run_both(reader, layer, plan, hidden, ids, weights, padding=None, threshold=
         None if padding is None else padding.to(DEVICE),
     )
     torch.cuda.synchronize()
-    expected = oracle.forward(
+    # token ranges on separate cores (every stage is per token)
+    expected = oracle.forward_parallel(
         oracle_weights(layer, reader),
         bits(hidden),
         ids.cpu().numpy(),
@@ -372,3 +373,64 @@ def test_large_batch_selection_is_top_f_of_own_scores():
     order = scores.argsort(dim=1, descending=True, stable=True)[:, : plan.final_count]
     membership = torch.zeros_like(scores, dtype=torch.bool).scatter_(1, order, True)
     assert torch.equal(reader.selected[:tokens].cpu(), membership)
+
+
+@pytest.fixture(scope="module")
+def skewed_qwen3_layer():
+    """C4: the Qwen3-30B-A3B shape at batch 256 with Zipf(1.2) expert popularity."""
+    return make_layer(hidden=2048, width=768, experts=128, top_k=8, rank=32, tokens=256,
+                      seed=80, zipf=1.2, device=DEVICE)
+
+
+@pytest.mark.parametrize("retention", [0.06, 0.123, 0.25])
+def test_skewed_routing_qwen3_batch_256(skewed_qwen3_layer, retention):
+    """Load-imbalanced routing (the hottest expert serves most tokens, many
+    experts none) over the retention sweep F = 369 / 756 / 1536: hot experts
+    split into many 16-pair tiles, cold ones hold one pair."""
+    layer = skewed_qwen3_layer
+    tokens = 256
+    counts = torch.bincount(layer.ids.reshape(-1).cpu(), minlength=128)
+    assert counts.max() > 64  # the hottest expert alone needs five or more tiles
+    plan = compile_budget(hidden_size=2048, expert_width=768, top_k=8, retention=retention,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+    # the grouping under skew: experts ascending, each expert's pairs in pair
+    # order cut into tiles of 16, every pair in exactly one tile slot
+    ws = reader.workspace
+    total = int(ws.group_total.item())
+    tile_experts = ws.group_experts[:total].cpu().numpy()
+    tile_counts = ws.group_counts[:total].cpu().numpy()
+    slots = ws.group_pairs[: 16 * total].cpu().numpy().reshape(total, 16)
+    pair_tiles = ws.pair_tiles[: tokens * 8].cpu().numpy()
+    sorted_ids = expected["ids"].reshape(-1)
+    assert (np.diff(tile_experts) >= 0).all()
+    order = np.concatenate([slots[z, : tile_counts[z]] for z in range(total)])
+    assert np.array_equal(np.sort(order), np.arange(tokens * 8))
+    for expert in np.unique(tile_experts):
+        members = np.concatenate([slots[z, : tile_counts[z]] for z in np.flatnonzero(tile_experts == expert)])
+        assert np.array_equal(members, np.flatnonzero(sorted_ids == expert))
+        assert (tile_counts[tile_experts == expert][:-1] == 16).all()
+    for z in range(total):
+        assert np.array_equal(pair_tiles[slots[z, : tile_counts[z]]], 16 * z + np.arange(tile_counts[z]))
+
+
+@pytest.fixture(scope="module")
+def fine_grained_layer():
+    """C5: 256 experts of width 512 (block-paired sketch tails) at batch 128."""
+    return make_layer(hidden=2048, width=512, experts=256, top_k=8, rank=32, tokens=128,
+                      seed=90, device=DEVICE)
+
+
+@pytest.mark.parametrize("keep", [1.0, 0.625])
+def test_fine_grained_experts_batch_128(fine_grained_layer, keep):
+    """Point-only screening over every coordinate (keep 1.0) against the
+    two-stage screen that keeps 80 of 128 rotated coordinates per block."""
+    layer = fine_grained_layer
+    tokens = 128
+    plan = compile_budget(hidden_size=2048, expert_width=512, top_k=8, retention=0.123,
+                          screen_keep=keep)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)

@@ -406,3 +406,18 @@ def test_dense_stock_on_retained_subset():
         routed = torch.from_numpy(
             (r["values"][t] * r["weights"][t][:, None]).sum(0)).double()
         torch.testing.assert_close(routed, dense, rtol=1e-2, atol=2e-3)
+
+
+def test_token_parallel_oracle_equals_one_call():
+    """Token ranges in threads give the single call's results (every stage is per token)."""
+    layer = small_layer(tokens=7, seed=27)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    padding = np.array([0, 1, 0, 0, 1, 0, 0], np.uint8)
+    args = (cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(), layer.weights.numpy())
+    whole = oracle.forward(*args, final_count=plan.final_count, keep=80, padding=padding)
+    split = oracle.forward_parallel(*args, final_count=plan.final_count, keep=80,
+                                    padding=padding, workers=3)
+    assert whole.keys() == split.keys()
+    for key in whole:
+        assert np.array_equal(whole[key], split[key]), key
