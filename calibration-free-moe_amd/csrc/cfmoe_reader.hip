@@ -1640,9 +1640,16 @@ group_exact_kernel(GroupExactArgs a) {
   const int count = load_uniform(a.group_counts + z);
   const i32x16 slots = load_uniform(reinterpret_cast<const i32x16 *>(a.group_pairs + kGroupPairs * z));
   const uint32_t mask_word = load_uniform(a.tile_masks + static_cast<long>(z) * a.I + c);
-  // all five issued before any is tested (else each waits under its branch)
-  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots), "s"(mask_word));
+  // the neighbouring tiles' experts: an expert split into several tiles has
+  // its rows read by each of them (entries past the count are never used)
+  const int bound = a.tile_items / a.channel_groups;
+  const int before = load_uniform(a.group_experts + max(z - 1, 0));
+  const int after = load_uniform(a.group_experts + min(z + 1, bound - 1));
+  // all issued before any is tested (else each waits under its branch)
+  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots), "s"(mask_word), "s"(before),
+               "s"(after));
   if (z >= total) return;
+  const bool shared_rows = (z > 0 && before == e) || (z + 1 < total && after == e);
   // lane p < count: pair p of the tile
   int pair = slots[0];
 #pragma unroll
@@ -1668,11 +1675,21 @@ group_exact_kernel(GroupExactArgs a) {
   };
   // the first keeping pair's hidden row travels with the gate/up rows
   load_hidden(__builtin_ctz(mask));
+  // rows read once stream past the caches; rows the expert's other tiles read
+  // again stay cached for them
   uint4 gw[kParts], uw[kParts];
+  if (shared_rows) {
 #pragma unroll
-  for (int j = 0; j < kParts; ++j) {
-    gw[j] = buffer_stream16(gate_rows, offset + 1024 * j);
-    uw[j] = buffer_stream16(up_rows, offset + 1024 * j);
+    for (int j = 0; j < kParts; ++j) {
+      gw[j] = buffer_load16(gate_rows, offset + 1024 * j);
+      uw[j] = buffer_load16(up_rows, offset + 1024 * j);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kParts; ++j) {
+      gw[j] = buffer_stream16(gate_rows, offset + 1024 * j);
+      uw[j] = buffer_stream16(up_rows, offset + 1024 * j);
+    }
   }
   // lane p holds pair p's sums; the results are stored after the loop (a
   // store inside it would delay the next pair's loads, which wait in order)
