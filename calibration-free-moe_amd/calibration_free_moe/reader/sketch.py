@@ -6,8 +6,9 @@ coordinate mask (:53-68), the packed sketch format (:84-150), its decoder
 (:209-232), the differentiable sketch feature (:153-206) and the recovery-map
 acquisition check (:71-81). The packed format is an interface shared with
 prebuilt sketches and offline recovery fitting, so its byte layout follows the
-reference exactly; the construction here is vectorised over experts in chunks
-and runs on whatever device holds the weights.
+reference exactly. Device (GPU) weights are sketched by one HIP launch
+(cfmoe_build_sketch in the reader's library); host weights by the torch
+construction here, vectorised over experts in chunks.
 
 Layout of one expert's codes (rows = 2 I, blocks = H / 128, stride =
 `sketch_code_stride(rows)`, body = stride rounded down to 32, tail = stride %
@@ -153,6 +154,14 @@ def build_sketch(
         raise ValueError(
             "Ternary sketch requires 128-coordinate blocks and paired gate/up rows"
         )
+    if weights.is_cuda:
+        return _build_sketch_device(weights, signs)
+    return _build_sketch_torch(weights, signs, chunk)
+
+
+def _build_sketch_torch(weights: Tensor, signs: Tensor | None, chunk: int = 8) -> tuple[Tensor, Tensor]:
+    """The torch construction of build_sketch (any device), `chunk` experts at a time."""
+    experts, rows, hidden = weights.shape
     blocks, width = hidden // 128, rows // 2
     stride = sketch_code_stride(rows)
     body = stride - stride % 32
@@ -192,6 +201,43 @@ def build_sketch(
                 .transpose(2, 3)
                 .reshape(end - begin, -1)
             )
+    return codes, physical.permute(0, 3, 1, 2)
+
+
+def _build_sketch_device(weights: Tensor, signs: Tensor | None) -> tuple[Tensor, Tensor]:
+    """build_sketch of a device tensor: one HIP launch (cfmoe_build_sketch).
+
+    Same format and rule as the torch construction below it; the sums of
+    mean|v|, the scale and the residual run in the kernel's order, so a trit
+    can differ only for |v| within an FP32 rounding of 0.7 mean|v|. Raises if
+    the HIP library is missing (no host fallback for device weights).
+    """
+    from calibration_free_moe.reader import _ext
+
+    experts, rows, hidden = weights.shape
+    device = weights.device
+    source = weights.detach()
+    if source.dtype != torch.bfloat16:
+        raise ValueError("device sketch construction reads BF16 gate/up rows")
+    source = source.contiguous()
+    rotation = None
+    if signs is not None:
+        rotation = signs.to(device=device, dtype=torch.int8).contiguous()
+        if rotation.numel() != hidden:
+            raise ValueError("rotation signs must have one entry per hidden coordinate")
+    codes = torch.full(
+        (experts, sketch_storage_bytes(rows, hidden)), ZERO_CODE, dtype=torch.uint8, device=device
+    )
+    physical = torch.empty((experts, hidden // 128, 2, rows), dtype=torch.float16, device=device)
+    with torch.cuda.device(device):
+        _ext.check(
+            _ext.library().cfmoe_build_sketch(
+                experts, rows // 2, hidden, source.data_ptr(),
+                None if rotation is None else rotation.data_ptr(),
+                codes.data_ptr(), physical.data_ptr(),
+                torch.cuda.current_stream(device).cuda_stream,
+            )
+        )
     return codes, physical.permute(0, 3, 1, 2)
 
 

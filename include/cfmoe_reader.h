@@ -174,6 +174,20 @@ CFMOE_API int64_t cfmoe_trit_plane_bytes(const cfmoe_dims *dims);
 CFMOE_API int cfmoe_pack_trit_planes(const cfmoe_dims *dims, const uint8_t *codes,
                                      uint32_t *trit_planes, cfmoe_stream stream);
 
+/* Build the resident ternary sketch of `experts` experts' gate/up rows
+ * (bf16 [experts, 2 width, hidden], hidden a multiple of 128) on the device:
+ * the reference's construction (build_sketch, sketch.py:84-150: rotation by
+ * `signs` [hidden] +-1 int8 or none when NULL, TWN ternarisation per
+ * 128-coordinate block, five trits per byte, body/tail byte layout) in one
+ * launch instead of its per-expert torch loop. `codes` [experts,
+ * sketch_storage_bytes] must hold 121 (five zero trits) in every byte before
+ * the call (the kernel writes only the bytes that carry channels);
+ * `statistics` is fp16 in the physical [experts, hidden / 128, 2, 2 width]
+ * layout (scale plane, residual plane). */
+CFMOE_API int cfmoe_build_sketch(int32_t experts, int32_t width, int32_t hidden,
+                                 const void *gate_up, const int8_t *signs, uint8_t *codes,
+                                 void *statistics, cfmoe_stream stream);
+
 /* Routing-independent input rotation ahead of the router
  * (progressive.py:3829-3873). A following cfmoe_forward with
  * CFMOE_INPUT_PREPARED set skips its own rotation. */
