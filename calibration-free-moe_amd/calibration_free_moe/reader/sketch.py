@@ -6,9 +6,10 @@ coordinate mask (:53-68), the packed sketch format (:84-150), its decoder
 (:209-232), the differentiable sketch feature (:153-206) and the recovery-map
 acquisition check (:71-81). The packed format is an interface shared with
 prebuilt sketches and offline recovery fitting, so its byte layout follows the
-reference exactly. Device (GPU) weights are sketched by one HIP launch
-(cfmoe_build_sketch in the reader's library); host weights by the torch
-construction here, vectorised over experts in chunks.
+reference exactly. BF16 device (GPU) weights are sketched by one HIP launch
+(cfmoe_build_sketch in the reader's library); host weights, and device weights
+in other formats, by the torch construction here, vectorised over experts in
+chunks.
 
 Layout of one expert's codes (rows = 2 I, blocks = H / 128, stride =
 `sketch_code_stride(rows)`, body = stride rounded down to 32, tail = stride %
@@ -154,8 +155,9 @@ def build_sketch(
         raise ValueError(
             "Ternary sketch requires 128-coordinate blocks and paired gate/up rows"
         )
-    if weights.is_cuda:
+    if weights.is_cuda and weights.dtype == torch.bfloat16:
         return _build_sketch_device(weights, signs)
+    # host weights, or device weights in another format (the kernel reads BF16)
     return _build_sketch_torch(weights, signs, chunk)
 
 
@@ -216,10 +218,7 @@ def _build_sketch_device(weights: Tensor, signs: Tensor | None) -> tuple[Tensor,
 
     experts, rows, hidden = weights.shape
     device = weights.device
-    source = weights.detach()
-    if source.dtype != torch.bfloat16:
-        raise ValueError("device sketch construction reads BF16 gate/up rows")
-    source = source.contiguous()
+    source = weights.detach().contiguous()
     rotation = None
     if signs is not None:
         rotation = signs.to(device=device, dtype=torch.int8).contiguous()
