@@ -1747,7 +1747,7 @@ struct DownArgs {
   int H, I, K, N, F, max_tiles;
 };
 
-constexpr int kDownOutputs = 4;  // outputs per down thread (H / 4 threads)
+constexpr int kDownOutputs = 8;  // outputs per down thread (H / 8 threads)
 
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 
@@ -1811,14 +1811,14 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   const int channel = valid ? logical % a.I : 0;
   const int o = tid * kDownOutputs;
   const bool outputs = o < a.H;
-  const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + min(o, a.H - 4);
-  uint2 w[kDownTile];
+  const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + min(o, a.H - 8);
+  uint4 w[kDownTile];
 #pragma unroll
   for (int jj = 0; jj < kDownTile; ++jj) {
     const int c = __builtin_amdgcn_readlane(channel, jj);
     const bool use = outputs && local && ((live >> jj) & 1u);
-    w[jj] = load_global(use ? reinterpret_cast<const uint2 *>(rows + static_cast<long>(c) * a.H)
-                            : reinterpret_cast<const uint2 *>(&kZeroVector));
+    w[jj] = load_global(use ? reinterpret_cast<const uint4 *>(rows + static_cast<long>(c) * a.H)
+                            : &kZeroVector);
   }
   const bool mine = (live >> (lane & (kDownTile - 1))) & 1u;
   const uint16_t act_bits =
@@ -1833,13 +1833,16 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   for (int jj = 0; jj < kDownTile; ++jj) {
     if (!((live >> jj) & 1u)) break;
     const float act = __uint_as_float(static_cast<uint32_t>(__builtin_amdgcn_readlane(act_lane, jj)));
-    acc[0] = fmaf(__uint_as_float(w[jj].x << 16), act, acc[0]);
-    acc[1] = fmaf(__uint_as_float(w[jj].x & 0xffff0000u), act, acc[1]);
-    acc[2] = fmaf(__uint_as_float(w[jj].y << 16), act, acc[2]);
-    acc[3] = fmaf(__uint_as_float(w[jj].y & 0xffff0000u), act, acc[3]);
+    const uint32_t wv[4] = {w[jj].x, w[jj].y, w[jj].z, w[jj].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc[2 * i] = fmaf(__uint_as_float(wv[i] << 16), act, acc[2 * i]);
+      acc[2 * i + 1] = fmaf(__uint_as_float(wv[i] & 0xffff0000u), act, acc[2 * i + 1]);
+    }
   }
   float *out = a.parts + (static_cast<long>(t) * a.max_tiles + tile) * a.H + o;
   *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  *reinterpret_cast<float4 *>(out + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
 }
 
 // ---------------------------------------------------------------------------
