@@ -1,0 +1,106 @@
+"""Operator paths the runtime reaches besides a plain call (needs an MI355X).
+
+* Early rotation: `prepare_input(hidden, padding)` then
+  `reader(..., input_prepared=True)`, the order the reference's vLLM binding
+  uses (runtime/experts.py:402-427, :497-505; progressive.py:3829-3873).
+* The default constructor, which builds the sketch itself (`sketch=None`).
+* The configurations without a test elsewhere: Qwen3-30B-A3B at batch 128 and
+  the 256-expert layer at batch 1, with point-only (keep 1.0) and two-stage
+  (keep 0.625) screening.
+
+Every case is held bit for bit to the CPU oracle on the reader's own tensors.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from calibration_free_moe.reader.budget import compile_budget
+from calibration_free_moe.reader.progressive import ProgressiveReader, channel_major_down
+from tests.synthetic import make_layer
+from tests.test_gpu_parity import DEVICE, assert_parity, build, run_both
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("tokens", [1, 24])
+def test_prepared_input_equals_a_plain_call(tokens):
+    """The prepared call reads the rotation that prepare_input left; a stale
+    rotation from an earlier call with other rows would change the result."""
+    layer = make_layer(hidden=512, width=256, experts=16, top_k=4, rank=16, tokens=tokens,
+                       seed=100 + tokens)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    hidden = layer.hidden.to(DEVICE)
+    ids, weights = layer.ids.to(DEVICE), layer.weights.to(DEVICE)
+    padding = torch.zeros(tokens, dtype=torch.bool, device=DEVICE)
+    padding[-1] = True
+    if tokens > 2:
+        padding[tokens // 3] = True
+    plain = reader(hidden, ids, weights, padding).clone()
+    torch.cuda.synchronize()
+    # leave another batch's rotation in the workspace
+    other = torch.randn(tokens, 512, generator=torch.Generator().manual_seed(7)).bfloat16()
+    reader(other.to(DEVICE), ids, weights)
+    assert reader.prepare_input(hidden, padding) is True
+    out = reader(hidden, ids, weights, padding, input_prepared=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    _, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights,
+                           padding.cpu())
+    # run_both made a plain call; redo the prepared one and compare its state
+    assert reader.prepare_input(hidden, padding)
+    out = reader(hidden, ids, weights, padding, input_prepared=True)
+    torch.cuda.synchronize()
+    assert_parity(reader, out, expected, tokens)
+
+
+def test_prepare_input_is_a_no_op_for_a_dense_plan():
+    layer = make_layer(hidden=256, width=64, experts=4, top_k=2, rank=8, tokens=2, seed=104)
+    plan = compile_budget(hidden_size=256, expert_width=64, top_k=2, retention=1.0)
+    reader = build(layer, plan, 2, selection_score="point")
+    assert reader.prepare_input(layer.hidden.to(DEVICE)) is False
+
+
+def test_default_constructor_builds_its_own_sketch():
+    """sketch=None: the reader builds the codes from its device weights (one
+    HIP launch) and screens with them; the oracle reads the same codes."""
+    tokens = 3
+    layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens,
+                       seed=105)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    reader = ProgressiveReader(
+        layer.gate_up.to(DEVICE), channel_major_down(layer.down.to(DEVICE)),
+        layer.encoder.to(DEVICE), layer.decoder.to(DEVICE), plan, tokens,
+        selection_score="point",
+    )
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+
+
+def test_qwen3_batch_128_bit_exact():
+    """C3 at batch 128: 1,024 routed pairs over 128 experts (grouped paths)."""
+    tokens = 128
+    layer = make_layer(hidden=2048, width=768, experts=128, top_k=8, rank=32, tokens=tokens,
+                       seed=73, device=DEVICE)
+    plan = compile_budget(hidden_size=2048, expert_width=768, top_k=8, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+
+
+@pytest.mark.parametrize("keep", [1.0, 0.625])
+def test_fine_grained_experts_batch_1(keep):
+    """C5 at batch 1: 256 experts of width 512 (block-paired sketch tails)."""
+    layer = make_layer(hidden=2048, width=512, experts=256, top_k=8, rank=32, tokens=1,
+                       seed=91, device=DEVICE)
+    plan = compile_budget(hidden_size=2048, expert_width=512, top_k=8, retention=0.123,
+                          screen_keep=keep)
+    reader = build(layer, plan, 1, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, 1)
+    assert int(reader.selected[0].sum()) == plan.final_count
+    np.testing.assert_array_equal(expected["counts"].sum(1), plan.final_count)

@@ -1,12 +1,24 @@
-"""Resident sketch: format, decoding and rotation (reference tests/test_sketch.py,
-tests/test_progressive_reader.py:33-99)."""
+"""Resident sketch: rotation, mask, packed format, statistics and the sketch
+feature, each against a construction written here from its definition.
+
+* Rotation: the Sylvester Hadamard matrix as an explicit float64 matrix.
+* Mask: a sort of (|v| descending, coordinate ascending).
+* Format: a numpy decoder that locates every trit by address (`stored_address`
+  of tests/test_budget.py) and reads its base-3 digit.
+* Ternarisation: a hand-made block with known trits, scale and residual, and
+  float64 restatements on random weights.
+* Feature: explicit float64 matrices for the projection and its gradient.
+"""
+
+import os
 
 import numpy as np
 import pytest
 import torch
 
-from calibration_free_moe.reader.budget import compile_budget
+from calibration_free_moe.reader.budget import sketch_storage_bytes
 from calibration_free_moe.reader.sketch import (
+    ZERO_CODE,
     block_hadamard_signs,
     build_sketch,
     differentiable_sketch_feature,
@@ -14,168 +26,209 @@ from calibration_free_moe.reader.sketch import (
     rotate_blocks,
     unpack_sketch,
 )
+from tests.test_budget import stored_address
 
-GOLDEN = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden")
-
-
-def independent_unpack(codes, rows, hidden):
-    """Decode codes by reassembling coordinate runs (no library offsets)."""
-    stride = (2 * ((rows // 2 + 4) // 5) + 15) // 16 * 16
-    body, blocks = stride // 32 * 32, hidden // 128
-    runs = codes[..., : blocks * 128 * body].reshape(codes.shape[0], blocks, 128, body)
-    if stride % 32:
-        tails = codes[..., blocks * 128 * body:].reshape(-1, (blocks + 1) // 2, 128, 2, 16)
-        tails = tails.transpose(2, 3).reshape(-1, (blocks + 1) // 2 * 2, 128, 16)[:, :blocks]
-        runs = torch.cat((runs, tails), dim=-1)
-    row = torch.arange(rows)
-    channel = row % (rows // 2)
-    trits = (runs[..., 2 * (channel // 5) + row // (rows // 2)].long() // (3 ** (channel % 5))) % 3 - 1
-    return trits.movedim(-1, -3).flatten(-2)
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 
 
-def hadamard128():
-    block = torch.ones(1, 1, dtype=torch.float64)
-    while len(block) < 128:
-        block = torch.cat((torch.cat((block, block), 1), torch.cat((block, -block), 1)), 0)
-    return block
+def sylvester(size: int = 128) -> np.ndarray:
+    matrix = np.ones((1, 1))
+    while len(matrix) < size:
+        matrix = np.block([[matrix, matrix], [matrix, -matrix]])
+    return matrix
+
+
+def rotation_matrix(signs: np.ndarray) -> np.ndarray:
+    """blockdiag(H128) diag(signs) / sqrt(128), float64."""
+    blocks = len(signs) // 128
+    h = sylvester()
+    full = np.zeros((len(signs), len(signs)))
+    for b in range(blocks):
+        full[128 * b:128 * (b + 1), 128 * b:128 * (b + 1)] = h
+    return full * signs[None, :].astype(np.float64) / np.sqrt(128.0)
+
+
+def decode_by_address(codes: np.ndarray, width: int, hidden: int) -> np.ndarray:
+    """Trits [E, 2 width, hidden] read one byte address at a time."""
+    experts = codes.shape[0]
+    rows = 2 * width
+    out = np.zeros((experts, rows, hidden), np.int8)
+    for row in range(rows):
+        plane, channel = divmod(row, width)
+        byte = 2 * (channel // 5) + plane
+        power = 3 ** (channel % 5)
+        for coordinate in range(hidden):
+            address = stored_address(width, hidden, coordinate // 128, coordinate % 128, byte)
+            out[:, row, coordinate] = (codes[:, address].astype(np.int64) // power) % 3 - 1
+    return out
+
+
+def twn(values: np.ndarray):
+    """Float64 TWN rule of one block: trits, scale, mean squared residual."""
+    magnitude = np.abs(values)
+    keep = magnitude > 0.7 * magnitude.mean()
+    trits = np.where(keep, np.sign(values), 0)
+    scale = magnitude[keep].mean() if keep.any() else 0.0
+    return trits, scale, np.mean((values - trits * scale) ** 2)
 
 
 def test_signs_match_committed_fixture():
     signs = block_hadamard_signs(2048, "cpu")
-    assert set(signs.unique().tolist()) == {-1, 1}
-    expected = np.load(f"{GOLDEN}/signs_2048.npy")
-    assert np.array_equal(signs.numpy(), expected)
-    assert torch.equal(block_hadamard_signs(256, "cpu"), signs[:256])
+    assert np.array_equal(signs.numpy(), np.load(os.path.join(GOLDEN, "signs_2048.npy")))
+    assert set(signs.tolist()) == {-1, 1}
+    # a prefix of a wider model's signs is the narrower model's signs
+    assert torch.equal(block_hadamard_signs(384, "cpu"), signs[:384])
 
 
-def test_ternary_packing_and_residual_variance():
-    # Unrotated known answer (reference test_progressive_reader.py:81-99).
-    torch.manual_seed(33)
-    weights = torch.randn(2, 8, 256).bfloat16()
-    codes, metadata = build_sketch(weights)
-    original = weights.float().reshape(2, 8, 2, 128)
-    keep = original.abs() > 0.7 * original.abs().mean(-1, keepdim=True)
-    expected_scale = (original.abs() * keep).sum(-1) / keep.sum(-1)
-    expected_codes = torch.where(keep, original.sign(), 0).reshape_as(weights)
-    assert torch.equal(independent_unpack(codes, 8, 256), expected_codes.long())
-    assert torch.equal(unpack_sketch(codes, 8, 256).long(), expected_codes.long())
-    assert torch.equal(metadata[..., 0], expected_scale.half())
-    residual = original - expected_codes.reshape_as(original) * expected_scale[..., None]
-    assert torch.equal(metadata[..., 1], residual.square().mean(-1).half())
-    assert codes.numel() + metadata.numel() * 2 == 2 * 2 * (128 * 16 + 8 * 4)
-    assert metadata.stride() == (4 * 4 * 2, 1, 4 * 4, 2 * 4)
+def test_rotation_is_the_explicit_hadamard_matrix():
+    signs = block_hadamard_signs(384, "cpu")
+    matrix = rotation_matrix(signs.numpy())
+    generator = torch.Generator().manual_seed(5)
+    # small integers: every butterfly sum is exact, so only the final FP32
+    # scaling rounds, once
+    x = torch.randint(-6, 7, (4, 384), generator=generator).float()
+    integer = np.rint(matrix * np.sqrt(128.0)).astype(np.int64)  # +-1 entries
+    exact = x.numpy().astype(np.int64) @ integer.T
+    want = exact.astype(np.float32) * np.float32(1 / np.sqrt(128.0))
+    assert np.array_equal(rotate_blocks(x, signs).numpy(), want)
+    y = torch.randn(3, 384, generator=generator)
+    np.testing.assert_allclose(rotate_blocks(y, signs).double().numpy(),
+                               y.double().numpy() @ matrix.T, rtol=0, atol=2e-6)
+    # the rotation is orthogonal: it keeps every row's norm
+    np.testing.assert_allclose(np.linalg.norm(rotate_blocks(y, signs).numpy(), axis=1),
+                               np.linalg.norm(y.numpy(), axis=1), rtol=1e-6)
+    assert torch.equal(rotate_blocks(y, None), y)
 
 
-@pytest.mark.parametrize("width,hidden", [(512, 384), (704, 256), (48, 256)])
-def test_sector_tiled_sketch_preserves_rows_and_prices_loads(width, hidden):
-    """Half-sector widths, an odd final block; walks every byte request."""
-    torch.manual_seed(83)
-    weights = torch.randn(1, 2 * width, hidden).bfloat16()
-    codes, _ = build_sketch(weights)
-    original = weights.float().reshape(1, 2 * width, hidden // 128, 128)
-    keep = original.abs() > 0.7 * original.abs().mean(-1, keepdim=True)
-    signed = torch.where(keep, original.sign(), 0)
-    assert torch.equal(unpack_sketch(codes, 2 * width, hidden), signed.flatten(-2).to(torch.int8))
-    assert torch.equal(independent_unpack(codes, 2 * width, hidden), signed.flatten(-2).long())
-    useful = 2 * ((width + 4) // 5)
-    stride = (useful + 15) // 16 * 16
-    body = stride // 32 * 32
-    blocks = hidden // 128
-    sectors = 0
-    for block in range(blocks):
-        for coordinate in range(80):
-            for start in range(0, useful, 32):
-                byte = torch.arange(start, min(start + 32, useful))
-                if start < body:
-                    address = (block * 128 + coordinate) * body + byte
-                else:
-                    address = (blocks * 128 * body + (block // 2 * 128 + coordinate) * 32
-                               + block % 2 * 16 + byte - body)
-                assert len(set((address // 32).tolist())) == 1
-                sectors += 1
-    plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=1, retention=0.1,
-                          screen_keep=0.625)
-    assert plan.sketch_read_bytes(residual=False) == sectors * 32 + blocks * 4 * width
+@pytest.mark.parametrize("keep", [1, 80, 127, 128])
+def test_mask_keeps_the_largest_magnitudes_lower_coordinates_first(keep):
+    generator = torch.Generator().manual_seed(keep)
+    # many exact ties in magnitude, including across signs
+    x = torch.randint(-3, 4, (5, 256), generator=generator).float()
+    got = mask_rotated_blocks(x, keep).reshape(-1, 128).numpy()
+    for row, values in enumerate(x.reshape(-1, 128).numpy()):
+        order = sorted(range(128), key=lambda c: (-abs(values[c]), c))
+        want = np.zeros(128, np.float32)
+        want[order[:keep]] = values[order[:keep]]
+        assert np.array_equal(got[row], want)
 
 
-def test_padding_byte_is_zero_code():
-    codes, _ = build_sketch(torch.randn(1, 2 * 48, 256).bfloat16())
-    stride = 32  # 2 * ceil(48 / 5) = 20 useful bytes, padded to 32
-    rows = codes.reshape(-1)[: 2 * 128 * stride].reshape(2 * 128, stride)
-    assert torch.all(rows[:, 20:] == 121)
+def test_known_block_ternarisation():
+    """One block whose trits, scale and residual are fixed by hand.
+
+    32 values of magnitude 4, 32 of 2, 64 of 1/2: mean |v| = 1.75, threshold
+    1.225, so the 4s and 2s are kept (scale 3) and the halves dropped; the
+    residual is (32 * 1 + 32 * 1 + 64 * 0.25) / 128 = 0.625.
+    """
+    block = np.array([4.0] * 32 + [2.0] * 32 + [0.5] * 64)
+    sign = np.where(np.arange(128) % 3 == 0, -1.0, 1.0)
+    values = np.zeros((1, 2, 256))
+    values[0, 0, :128] = block * sign  # gate row, block 0
+    values[0, 1, 128:] = -block * sign  # up row, block 1
+    codes, statistics = build_sketch(torch.from_numpy(values).bfloat16())
+    trits = decode_by_address(codes.numpy(), 1, 256)
+    assert np.array_equal(trits[0, 0, :128], np.where(block > 1.225, sign, 0))
+    assert np.array_equal(trits[0, 1, 128:], -np.where(block > 1.225, sign, 0))
+    assert not trits[0, 0, 128:].any() and not trits[0, 1, :128].any()
+    stats = statistics.float().numpy()  # [E, 2 I, blocks, 2]
+    assert stats[0, 0, 0].tolist() == [3.0, 0.625]
+    assert stats[0, 1, 1].tolist() == [3.0, 0.625]
+    assert stats[0, 0, 1].tolist() == [0.0, 0.0]
+    assert statistics.stride() == (4 * 2, 1, 4, 2)
 
 
-def test_rotation_is_the_scaled_sylvester_transform():
+@pytest.mark.parametrize("width,hidden,rotated", [(8, 256, False), (48, 384, True),
+                                                  (40, 128, False), (24, 512, True)])
+def test_codes_and_statistics_follow_the_rule(width, hidden, rotated):
+    """Random weights: the address decoder, the library decoder and a float64
+    TWN restatement agree; statistics to FP16 rounding. A trit may differ from
+    the float64 rule only where |v| sits within FP32 rounding of the threshold."""
+    generator = torch.Generator().manual_seed(width + hidden)
+    weights = (torch.randn(2, 2 * width, hidden, generator=generator) * 0.05).bfloat16()
+    signs = block_hadamard_signs(hidden, "cpu") if rotated else None
+    codes, statistics = build_sketch(weights, signs)
+    assert codes.shape == (2, sketch_storage_bytes(2 * width, hidden))
+    by_address = decode_by_address(codes.numpy(), width, hidden)
+    assert np.array_equal(unpack_sketch(codes, 2 * width, hidden).numpy(), by_address)
+    value = weights.double().numpy()
+    if rotated:
+        value = value @ rotation_matrix(signs.numpy()).T
+    blocks = value.reshape(2, 2 * width, hidden // 128, 128)
+    trits = by_address.reshape(blocks.shape)
+    stats = statistics.float().numpy()
+    for e in range(2):
+        for row in range(2 * width):
+            for b in range(hidden // 128):
+                want, scale, residual = twn(blocks[e, row, b])
+                near = np.abs(np.abs(blocks[e, row, b]) - 0.7 * np.abs(blocks[e, row, b]).mean())
+                differ = trits[e, row, b] != want
+                assert (near[differ] < 1e-6).all()
+                if not differ.any():
+                    np.testing.assert_allclose(stats[e, row, b], [scale, residual],
+                                               rtol=2e-3, atol=1e-7)
+
+
+def test_unused_bytes_hold_the_zero_code():
+    """Width 48: 2 ceil(48 / 5) = 20 code bytes per coordinate in a 32-byte
+    stride; bytes 20..31 are padding and decode to zero trits."""
+    codes, _ = build_sketch(torch.randn(1, 96, 256).bfloat16())
+    for coordinate in range(256):
+        for byte in range(20, 32):
+            address = stored_address(48, 256, coordinate // 128, coordinate % 128, byte)
+            assert codes[0, address] == ZERO_CODE
+
+
+def test_build_is_independent_of_chunking():
+    weights = torch.randn(5, 2 * 64, 256).bfloat16()
     signs = block_hadamard_signs(256, "cpu")
-    matrix = torch.block_diag(hadamard128(), hadamard128()) * signs.double()[None, :]
-    # Small dyadic integers: every butterfly sum is exact in FP32.
-    x = torch.randint(-4, 5, (5, 256)).float()
-    exact = (x.double() @ matrix.T) * float(np.float32(1 / np.sqrt(128)))
-    assert torch.equal(rotate_blocks(x, signs).double(), exact.float().double())
-    y = torch.randn(7, 256)
-    torch.testing.assert_close(
-        rotate_blocks(y, signs).double(), (y.double() @ matrix.T) / 128**0.5, rtol=1e-5, atol=1e-5
-    )
-    # Orthogonality
-    z = rotate_blocks(torch.eye(256), signs).double()
-    torch.testing.assert_close(z @ z.T, torch.eye(256, dtype=torch.float64), atol=1e-6, rtol=0)
-
-
-def test_mask_keeps_largest_with_coordinate_ties():
-    x = torch.randint(-3, 4, (6, 256)).float()
-    kept = mask_rotated_blocks(x, 80).reshape(-1, 128)
-    for row, values in enumerate(x.reshape(-1, 128).tolist()):
-        order = sorted(range(128), key=lambda c: (-abs(values[c]), c))[:80]
-        expected = torch.zeros(128)
-        expected[order] = torch.tensor(values)[order]
-        assert torch.equal(kept[row], expected)
+    whole = build_sketch(weights, signs, chunk=8)
+    split = build_sketch(weights, signs, chunk=2)
+    assert torch.equal(whole[0], split[0]) and torch.equal(whole[1], split[1])
 
 
 @pytest.mark.parametrize("keep", [80, 128])
 @pytest.mark.parametrize("input_is_rotated", [False, True])
-def test_sketch_feature_matches_kept_coordinate_reference(keep, input_is_rotated):
-    torch.manual_seed(71)
-    hidden, width = 256, 16
+def test_sketch_feature_and_its_gradient_from_explicit_matrices(keep, input_is_rotated):
+    hidden, width, tokens = 256, 16, 3
+    generator = torch.Generator().manual_seed(keep + input_is_rotated)
     signs = block_hadamard_signs(hidden, "cpu")
-    codes, statistics = build_sketch(torch.randn(1, 2 * width, hidden) * 0.1, signs=signs)
-    x = torch.randint(-3, 4, (3, hidden)).float().requires_grad_()
-    rotated = x if input_is_rotated else rotate_blocks(x, signs)
-    blocks = rotated.reshape(-1, 128)
-    mask = torch.zeros_like(blocks, dtype=torch.bool)
-    for row, values in enumerate(blocks.detach().tolist()):
-        order = sorted(range(128), key=lambda c: (-abs(values[c]), c))
-        mask[row, order[:keep]] = True
-    kept = torch.where(mask, blocks, 0.0).reshape(3, 2, 128)
-    trits = unpack_sketch(codes, 2 * width, hidden)[0].float().reshape(2 * width, 2, 128)
-    projection = (torch.einsum("tbc,rbc->trb", kept, trits) * statistics[0, ..., 0].float()).sum(-1)
-    g, u = projection.chunk(2, dim=-1)
-    expected = (torch.nn.functional.silu(g.bfloat16().float()) * u.bfloat16().float()).bfloat16()
-    actual = differentiable_sketch_feature(
-        x, codes[0], statistics[0], signs, input_is_rotated=input_is_rotated,
-        screen_coordinates=keep,
-    )
-    torch.testing.assert_close(actual, expected)
-    expected_grad = torch.autograd.grad(expected.float().sum(), x)[0]
-    actual_grad = torch.autograd.grad(actual.float().sum(), x)[0]
-    torch.testing.assert_close(actual_grad, expected_grad)
-    if input_is_rotated:
-        assert torch.count_nonzero(actual_grad.reshape_as(mask)[~mask]) == 0
-
-
-def test_rotated_build_matches_unrotated_build_of_rotated_rows():
-    torch.manual_seed(7)
-    signs = block_hadamard_signs(256, "cpu")
-    weights = torch.randn(3, 2 * 32, 256).bfloat16()
-    codes, stats = build_sketch(weights, signs)
-    rotated = rotate_blocks(weights.float().reshape(-1, 256), signs).reshape(3, 64, 256)
-    codes2, stats2 = build_sketch(rotated)
-    assert torch.equal(codes, codes2)
-    assert torch.equal(stats, stats2)
-
-
-def test_chunked_build_is_chunk_independent():
-    weights = torch.randn(5, 2 * 64, 256).bfloat16()
-    signs = block_hadamard_signs(256, "cpu")
-    a = build_sketch(weights, signs, chunk=1)
-    b = build_sketch(weights, signs, chunk=8)
-    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    codes, statistics = build_sketch(
+        torch.randn(1, 2 * width, hidden, generator=generator) * 0.1, signs=signs)
+    x = torch.randn(tokens, hidden, generator=generator, dtype=torch.float32)
+    feature = differentiable_sketch_feature(
+        x.clone().requires_grad_(), codes[0], statistics[0], signs,
+        input_is_rotated=input_is_rotated, screen_coordinates=keep)
+    # explicit matrices: sketch S [2I, H] (trit * block scale), rotation R, mask M(x)
+    trits = decode_by_address(codes.numpy(), width, hidden)[0].astype(np.float64)
+    scale = np.repeat(statistics[0, :, :, 0].double().numpy(), 128, axis=1)
+    sketch = trits * scale
+    rotation = np.eye(hidden) if input_is_rotated else rotation_matrix(signs.numpy())
+    xs = x.double().numpy()
+    for t in range(tokens):
+        rotated = rotation @ xs[t]
+        kept = np.zeros(hidden, bool)
+        for b in range(hidden // 128):
+            values = rotated[128 * b:128 * (b + 1)]
+            order = sorted(range(128), key=lambda c: (-abs(values[c]), c))[:keep]
+            kept[128 * b + np.array(order)] = True
+        projection = sketch @ np.where(kept, rotated, 0.0)
+        g, u = projection[:width], projection[width:]
+        g16 = torch.tensor(g).float().bfloat16().double().numpy()
+        u16 = torch.tensor(u).float().bfloat16().double().numpy()
+        sigma = 1 / (1 + np.exp(-g16))
+        want = g16 * sigma * u16
+        np.testing.assert_allclose(feature[t].double().detach().numpy(), want,
+                                   rtol=2e-2, atol=1e-3)
+        # d sum(phi(g) u) / dx = (A_g^T (phi'(g) u) + A_u^T phi(g)), A = S M R
+        a = sketch * kept[None, :] @ rotation
+        slope = sigma * (1 + g16 * (1 - sigma))
+        gradient = a[:width].T @ (slope * u16) + a[width:].T @ (g16 * sigma)
+        xt = x[t:t + 1].clone().requires_grad_()
+        value = differentiable_sketch_feature(
+            xt, codes[0], statistics[0], signs, input_is_rotated=input_is_rotated,
+            screen_coordinates=keep)
+        (got,) = torch.autograd.grad(value.float().sum(), xt)
+        np.testing.assert_allclose(got[0].double().numpy(), gradient, rtol=3e-2,
+                                   atol=3e-3 * np.abs(gradient).max())
+        if input_is_rotated:
+            assert not got[0].numpy()[~kept].any()
