@@ -83,6 +83,35 @@ def aligned_blocks(pairs: int, experts: int) -> int:
     return (aligned_pairs(pairs, experts) + GROUP_ROWS - 1) // GROUP_ROWS
 
 
+@torch.no_grad()
+def recovery_geometry(down: Tensor, norms: Tensor, encoder_t: Tensor, decoder: Tensor) -> Tensor:
+    """Where the recovery map sends each channel, relative to its down column.
+
+    Channel c of expert e has down column d = D_e[:, c] and recovery response
+    r = U b, with b = encoder_t[e, c] (the rank-R encoder row) and U the
+    decoder [H, R]. alpha = <d, r> / |d| is the response along d (0 when
+    d = 0) and beta = sqrt(max(|r|^2 - alpha^2, 0)) its part across d, the
+    quantities of the recovery-aware score (progressive.py:3347-3373). Both are
+    formed from R-dimensional quantities, <d, U b> = b . (U^T d) and
+    |U b|^2 = b^T (U^T U) b, in float64 one expert at a time, so no [I, H]
+    response is materialised. Returns float32 [E, I, 2].
+    """
+    u = decoder.double()
+    gram = u.T @ u  # [R, R]
+    geometry = torch.empty(
+        (down.shape[0], down.shape[2], 2), device=down.device, dtype=torch.float32
+    )
+    for expert in range(down.shape[0]):
+        b = encoder_t[expert].double()  # [I, R]
+        along = (b * (down[expert].double().T @ u)).sum(-1)  # <d_c, U b_c>
+        norm = norms[expert].double()
+        alpha = torch.where(norm > 0, along / torch.where(norm > 0, norm, 1.0), 0.0)
+        energy = ((b @ gram) * b).sum(-1)  # |U b_c|^2
+        geometry[expert, :, 0] = alpha.float()
+        geometry[expert, :, 1] = (energy - alpha.square()).clamp_min(0).sqrt().float()
+    return geometry
+
+
 def _next_power_of_2(value: int) -> int:
     return 1 if value <= 1 else 1 << (value - 1).bit_length()
 
@@ -566,20 +595,7 @@ class ProgressiveReader:
 
     def _geometry(self, down: Tensor) -> Tensor:
         """alpha, beta of each channel's recovery response (progressive.py:3347-3373)."""
-        e, _, i = down.shape
-        geometry = torch.zeros((e, i, 2), device=down.device, dtype=torch.float32)
-        decoder_float = self.decoder.float().T
-        for expert in range(e):
-            original = down[expert].float().T
-            response = self.encoder[expert].float() @ decoder_float
-            norm = self.norms[expert]
-            alpha = (original * response).sum(-1) / torch.where(
-                norm > 0, norm, torch.ones_like(norm)
-            )
-            beta = (response.square().sum(-1) - alpha.square()).clamp_min(0).sqrt()
-            geometry[expert, :, 0].copy_(alpha)
-            geometry[expert, :, 1].copy_(beta)
-        return geometry
+        return recovery_geometry(down, self.norms, self.encoder, self.decoder)
 
     def _fixed_charges(self, grouped: bool, grouped_screen: bool) -> tuple[float, ...]:
         """Per-token read statistics independent of the selection (slots 0-17).

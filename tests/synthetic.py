@@ -16,6 +16,7 @@ import numpy as np
 import torch
 from torch import Tensor
 
+from calibration_free_moe.reader.progressive import recovery_geometry
 from calibration_free_moe.reader.sketch import block_hadamard_signs, build_sketch
 
 
@@ -103,6 +104,41 @@ def make_layer(*, hidden: int, width: int, experts: int, top_k: int, rank: int,
                  x.to(device), ids.to(device), weights.to(device))
 
 
+def make_routed_layer(*, hidden: int, width: int, experts: int, top_k: int, rank: int,
+                      tokens: int, seed: int, std: float = 0.02) -> Layer:
+    """A full-width layer whose weights exist only for the routed experts.
+
+    The router and hidden states come first; then each expert some token routes
+    to gets its own seeded N(0, std^2) gate/up and down rows, the others stay
+    zero (their sketch codes are the zero code). The recovery map is the bank
+    of the routed experts. A token's computation reads nothing else, so this
+    is the per-token work of a benchmark shape at a fraction of the set-up
+    cost (CPU only).
+    """
+    generator = torch.Generator().manual_seed(seed)
+    router = (torch.randn(experts, hidden, generator=generator) * std).to(torch.bfloat16)
+    x = hidden_states(tokens, hidden, generator)
+    ids, weights = route(x, router, top_k)
+    gate_up = torch.zeros(experts, 2 * width, hidden, dtype=torch.bfloat16)
+    down = torch.zeros(experts, hidden, width, dtype=torch.bfloat16)
+    used = sorted(set(ids.reshape(-1).tolist()))
+    for e in used:
+        own = torch.Generator().manual_seed(seed * 100003 + e)
+        gate_up[e] = (torch.randn(2 * width, hidden, generator=own) * std).to(torch.bfloat16)
+        down[e] = (torch.randn(hidden, width, generator=own) * std).to(torch.bfloat16)
+    index = torch.tensor(used)
+    encoder_used, decoder = recovery_bank(down[index], rank)
+    encoder = torch.zeros(experts, rank, width, dtype=torch.bfloat16)
+    encoder[index] = encoder_used
+    codes_used, stats_used = build_sketch(gate_up[index], block_hadamard_signs(hidden, "cpu"))
+    codes = torch.full((experts, codes_used.shape[1]), 121, dtype=torch.uint8)
+    codes[index] = codes_used
+    statistics = torch.zeros((experts, hidden // 128, 2, 2 * width), dtype=torch.float16)
+    statistics[index] = stats_used.permute(0, 2, 3, 1)
+    statistics = statistics.permute(0, 3, 1, 2)
+    return Layer(gate_up, down, encoder, decoder, codes, statistics, router, x, ids, weights)
+
+
 def bits(tensor: Tensor) -> np.ndarray:
     """uint16 bit patterns of a BF16/FP16 tensor (CPU copy)."""
     return tensor.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
@@ -137,16 +173,7 @@ def cpu_weights(layer: Layer, point: bool = True):
     encoder_t = layer.encoder.transpose(1, 2).contiguous()
     geometry = None
     if not point:
-        decoder_float = layer.decoder.float().T
-        geometry = torch.zeros(down.shape[0], down.shape[2], 2)
-        for expert in range(down.shape[0]):
-            response = encoder_t[expert].float() @ decoder_float
-            original = down[expert].T
-            norm = norms[expert]
-            alpha = (original * response).sum(-1) / torch.where(norm > 0, norm, torch.ones_like(norm))
-            beta = (response.square().sum(-1) - alpha.square()).clamp_min(0).sqrt()
-            geometry[expert, :, 0] = alpha
-            geometry[expert, :, 1] = beta
+        geometry = recovery_geometry(layer.down, norms, encoder_t, layer.decoder)
     physical = layer.statistics.permute(0, 2, 3, 1).contiguous()
     hidden = layer.gate_up.shape[2]
     return oracle.Weights(

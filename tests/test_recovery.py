@@ -1,0 +1,33 @@
+"""Recovery map helpers against their definitions (CPU).
+
+`recovery_geometry` forms alpha and beta from R-dimensional quantities; here
+they are recomputed from the materialised per-channel response U b_c.
+"""
+
+import torch
+
+from calibration_free_moe.reader.progressive import recovery_geometry
+
+
+def test_geometry_equals_the_materialised_response():
+    generator = torch.Generator().manual_seed(3)
+    experts, hidden, width, rank = 3, 256, 48, 8
+    down = (torch.randn(experts, hidden, width, generator=generator) * 0.02).bfloat16()
+    down[1, :, 5] = 0  # a zero down column: alpha is 0, beta is |U b|
+    encoder_t = (torch.randn(experts, width, rank, generator=generator) * 0.1).bfloat16()
+    decoder = torch.linalg.qr(torch.randn(hidden, rank, generator=generator))[0].bfloat16()
+    norms = down.float().square().sum(1).sqrt()
+    got = recovery_geometry(down, norms, encoder_t, decoder).double()
+    for e in range(experts):
+        response = encoder_t[e].double() @ decoder.double().T  # [I, H]: U b_c
+        column = down[e].double().T  # [I, H]: d_c
+        length = column.norm(dim=-1)
+        alpha = torch.where(length > 0, (column * response).sum(-1) / length.clamp_min(1e-300), 0.0)
+        beta = (response.norm(dim=-1).square() - alpha.square()).clamp_min(0).sqrt()
+        torch.testing.assert_close(got[e, :, 0], alpha, rtol=1e-5, atol=1e-7)
+        torch.testing.assert_close(got[e, :, 1], beta, rtol=1e-5, atol=1e-7)
+    assert got[1, 5, 0] == 0
+    # alpha^2 + beta^2 = |U b|^2 (Pythagoras along and across d_c)
+    energy = (encoder_t.double() @ decoder.double().T).square().sum(-1)
+    torch.testing.assert_close(got[..., 0].square() + got[..., 1].square(), energy,
+                               rtol=1e-5, atol=1e-9)
