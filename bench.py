@@ -33,6 +33,7 @@ import torch  # noqa: E402
 from calibration_free_moe.reader import _ext  # noqa: E402
 from calibration_free_moe.reader.budget import compile_budget  # noqa: E402
 from calibration_free_moe.reader.progressive import (  # noqa: E402
+    GROUPED_TOKENS,
     ProgressiveReader,
     ReaderWorkspace,
     channel_major_down,
@@ -160,7 +161,7 @@ DIRECT_RANK = 32  # rank at which grouped batches run the encoder inside the exa
 STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "group_screen_kernel",
                  "score": "score_kernel", "select": "select_kernel", "exact": "exact_kernel",
                  "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
-GROUP_EXACT_TOKENS = 16  # batches from which the exact stage runs group_exact_kernel
+GROUP_EXACT_TOKENS = GROUPED_TOKENS  # batches from which the exact stage runs group_exact_kernel
 
 
 def encoder_in_exact(tokens: int, rank: int) -> bool:
@@ -409,8 +410,28 @@ def run_config(name: str, args, device) -> dict:
     }
 
 
+def cpu_threads() -> int:
+    """Threads of this process's CPU share: the affinity set, at most the
+    OpenMP thread setting of the box (16 per GPU)."""
+    available = len(os.sched_getaffinity(0))
+    return max(1, min(available, int(os.environ.get("OMP_NUM_THREADS") or available)))
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(seconds: float) -> dict:
-    """The CPU oracle (C, one thread) on the C1 layer: OLMoE shape, batch 1."""
+    """The CPU oracle (C, OpenMP over the CPU share) on the C1 layer: OLMoE
+    shape, batch 1; two warm-up calls, then the median of at least ten over
+    about `seconds`."""
     from oracle import oracle
     from tests.synthetic import bits
 
@@ -433,20 +454,24 @@ def cpu_baseline(seconds: float) -> dict:
     x = bits(data["hidden"])
     ids = data["ids"].cpu().numpy()
     w = data["weights"].cpu().numpy()
+    threads = cpu_threads()
     runs = []
     for _ in range(2):
-        oracle.forward(weights, x, ids, w, final_count=plan.final_count, keep=80)
+        oracle.forward(weights, x, ids, w, final_count=plan.final_count, keep=80, threads=threads)
     deadline = time.perf_counter() + seconds
     while time.perf_counter() < deadline or len(runs) < 10:
         begin = time.perf_counter()
-        oracle.forward(weights, x, ids, w, final_count=plan.final_count, keep=80)
+        oracle.forward(weights, x, ids, w, final_count=plan.final_count, keep=80, threads=threads)
         runs.append(time.perf_counter() - begin)
     return {
         "value": statistics.median(runs) * 1e6,
         "unit": "us/layer",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": f"C1 OLMoE-shaped layer, batch 1, median of {len(runs)} oracle calls",
+        "cpu_model": cpu_model(),
+        "logical_cpus_visible": os.cpu_count(),
+        "sample": f"C1 OLMoE-shaped layer, batch 1, median of {len(runs)} oracle calls "
+                  f"after 2 warm-ups ({threads} OpenMP threads)",
         "gbps_on_algorithmic_bytes": 17_804_352 / statistics.median(runs) / 1e9,
     }
 
@@ -550,7 +575,7 @@ def main() -> int:
     parser.add_argument("--layers", type=int, default=0)
     parser.add_argument("--tokens", type=int, default=0)
     parser.add_argument("--extra",
-                        default="c3:1,c3:32,c3:128,c4:256,c4:256:0.06,c4:256:0.25,"
+                        default="c1:1,c3:1,c3:32,c3:128,c4:256,c4:256:0.06,c4:256:0.25,"
                                 "c5:1,c5:128,c5:1:0.123:1.0,c5:128:0.123:1.0",
                         help="comma list of config:tokens[:retention[:screen_keep]] "
                              "measured beside the headline")
@@ -601,6 +626,7 @@ def main() -> int:
             "retention": retention, "screen_keep": keep, "rank": 32,
             "selection_score": "point", "final_count": headline["final_count"],
         },
+        "us_per_layer_median_step": round(headline["us_per_layer_median_event"], 3),
         "tokens_per_s": round(headline["tokens_per_s"], 1),
         "achieved_gbps": round(headline["achieved_gbps"], 1),
         "algorithmic_bytes_per_layer": headline["bytes_per_layer"],
@@ -625,7 +651,7 @@ def main() -> int:
              if key in ("name", "description", "layers", "tokens", "retention", "screen_keep",
                         "zipf", "final_count", "us_per_layer", "tokens_per_s", "achieved_gbps",
                         "layer_roofline_frac", "dominant", "dominant_gbps", "stage_us",
-                        "shared_expert_us_per_layer")}
+                        "shared_expert_us_per_layer", "us_per_layer_median_event")}
             for x in extras
         ],
     }

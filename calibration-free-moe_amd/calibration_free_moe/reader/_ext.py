@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 POINT = 1
 GELU = 2
@@ -40,6 +40,7 @@ class Dims(ctypes.Structure):
         ("final_count", ctypes.c_int32),
         ("keep", ctypes.c_int32),
         ("flags", ctypes.c_uint32),
+        ("grouped_tokens", ctypes.c_int32),
     ]
 
 

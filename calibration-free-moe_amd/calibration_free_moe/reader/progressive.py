@@ -56,8 +56,11 @@ def channel_major_down(weight: Tensor) -> Tensor:
 
 # (token, expert) pairs per expert-major block (progressive.py:80-81).
 GROUP_ROWS = 16
-# Batch sizes from which the reference runs expert-major (progressive.py:82-86).
-GROUPED_TOKENS = 32
+# Batch size from which the kept channels are computed expert-major (the
+# reference's crossover, progressive.py:82-86, is 32 on its GPUs; on MI355X
+# the grouped rows already pay at 16 tokens). The screen is expert-major at
+# every batch size here, so GROUPED_SCREEN_TOKENS only keeps the API.
+GROUPED_TOKENS = 16
 GROUPED_SCREEN_TOKENS = 64
 # Radix selection constants of the reference's small-batch path
 # (progressive.py:106-114); reported by `report()`.
@@ -120,7 +123,8 @@ def _screen_splits(hidden: int) -> int:
     return min(8, hidden // 128)
 
 
-def _dims(plan: BudgetPlan, experts: int, rank: int, flags: int = 0) -> _ext.Dims:
+def _dims(plan: BudgetPlan, experts: int, rank: int, flags: int = 0,
+          grouped_tokens: int = GROUPED_TOKENS) -> _ext.Dims:
     return _ext.Dims(
         plan.hidden_size,
         plan.expert_width,
@@ -130,6 +134,7 @@ def _dims(plan: BudgetPlan, experts: int, rank: int, flags: int = 0) -> _ext.Dim
         plan.final_count,
         plan.screen_coordinates,
         flags,
+        grouped_tokens,
     )
 
 
@@ -259,8 +264,10 @@ class ReaderWorkspace:
             (0, 1 << RADIX_HASH_BITS, RADIX_CAPACITY), dtype=torch.int32, device=device
         )
         self.keys = torch.empty((0, k), dtype=torch.int32, device=device)
-        self.pairs = torch.empty((0,), dtype=torch.int32, device=device)
-        self.block_experts = torch.empty((0,), dtype=torch.int32, device=device)
+        # the reference's expert-sorted pair list and block experts are the
+        # grouping's tile slots and tile experts here
+        self.pairs = self.group_pairs
+        self.block_experts = self.group_experts
         self.padded_pairs = torch.empty((1,), dtype=torch.int32, device=device)
         self.unions = torch.empty((0, 0, i), dtype=torch.int32, device=device)
         self.union_counts = torch.empty((0, 0, 2), dtype=torch.int32, device=device)
@@ -590,7 +597,16 @@ class ProgressiveReader:
         )
         self._workspace_c = workspace.pointers(self.read_work)
         self._workspace_c.next_ids = _pointer(self.candidate_ids[1])
-        self._charges = (ctypes.c_double * 18)(*self._fixed_charges(False, False))
+        # per-token read charges of per-token and of grouped calls; thresholded
+        # readers add theirs from the selection (the device still adds its
+        # per-tile and union terms)
+        charges = (ctypes.c_double * 18)
+        self._charges = {
+            grouped: charges(*(
+                self._fixed_charges(grouped, grouped) if selection_threshold is None
+                else (0.0,) * 18))
+            for grouped in (False, True)
+        }
         _ext.library()
 
     def _geometry(self, down: Tensor) -> Tensor:
@@ -600,8 +616,16 @@ class ProgressiveReader:
     def _fixed_charges(self, grouped: bool, grouped_screen: bool) -> tuple[float, ...]:
         """Per-token read statistics independent of the selection (slots 0-17).
 
-        Follows progressive.py:4492-4524 and the per-token encoder charge of
-        `_account_fixed` (progressive.py:265-269).
+        Slots 0-10 and 17 follow progressive.py:4492-4524. The requested-byte
+        slots 11-16 describe this build's kernels: the screen streams each
+        tile's trit planes (slot 11, with its matrix-core MACs in slot 15,
+        both added per tile on the device); the exact rows request 4 H bytes
+        per kept channel and token, or per channel of a tile's union in grouped
+        calls (slot 12, then counted on the device); the down rows request
+        2 H bytes per kept channel and token at every batch size (slot 13); the
+        recovery encoder requests the 2 R byte rows of all I channels of each
+        routed slot (slot 14); slot 16 counts the tokens of grouped calls.
+        `grouped_screen` is accepted for the reference's signature.
         """
         p = self.plan
         native = p.selected_weight_bytes()
@@ -610,11 +634,8 @@ class ProgressiveReader:
         residual = self.selection_score != "point"
         sketch = p.sketch_read_bytes(residual)
         h, unit = p.hidden_size, 2
-        encoder = (
-            2 * self.rank * (p.candidate_count - p.final_count)
-            if not grouped and self.rank > 0
-            else 0
-        )
+        encoder = 2 * self.rank * p.candidate_count
+        screened = p.completion_count < p.candidate_count
         return tuple(
             float(v)
             for v in (
@@ -628,10 +649,10 @@ class ProgressiveReader:
                 recovery,
                 0,
                 selection,
-                h if p.completion_count < p.candidate_count else 0,
-                0 if grouped_screen else sketch,
+                h if screened else 0,
+                0,
                 0 if grouped else unit * 2 * h * p.completion_count,
-                0 if grouped else unit * h * p.final_count,
+                unit * h * p.final_count,
                 encoder,
                 0,
                 int(grouped),
@@ -649,8 +670,7 @@ class ProgressiveReader:
             flags |= _ext.GEOMETRY
         if self.selection_threshold is not None:
             flags |= _ext.THRESHOLD
-        else:
-            flags |= _ext.ACCOUNT
+        flags |= _ext.ACCOUNT
         if ids.dtype == torch.int64:
             flags |= _ext.IDS_INT64
         if weights.dtype == torch.bfloat16:
@@ -696,7 +716,7 @@ class ProgressiveReader:
         if p.completion_count == p.candidate_count:
             return False
         tokens = self._validate_input(hidden, padding)
-        dims = _dims(p, self.native_gu.shape[0], self.rank, 0)
+        dims = _dims(p, self.native_gu.shape[0], self.rank, 0, self.grouped_tokens)
         _ext.check(
             _ext.library().cfmoe_prepare_input(
                 ctypes.byref(dims),
@@ -759,6 +779,7 @@ class ProgressiveReader:
             self.native_gu.shape[0],
             self.rank,
             self._flags(ids, weights, input_prepared and screened),
+            self.grouped_tokens,
         )
         _ext.check(
             _ext.library().cfmoe_forward(
@@ -771,7 +792,7 @@ class ProgressiveReader:
                 _pointer(padding),
                 out.data_ptr(),
                 tokens,
-                self._charges,
+                self._charges[tokens >= self.grouped_tokens],
                 self._stream(),
             )
         )
@@ -796,7 +817,7 @@ class ProgressiveReader:
         """
         tokens = hidden.shape[0]
         flags = self._flags(ids, weights, False) & ~_ext.ACCOUNT
-        dims = _dims(self.plan, self.native_gu.shape[0], self.rank, flags)
+        dims = _dims(self.plan, self.native_gu.shape[0], self.rank, flags, self.grouped_tokens)
         _ext.check(
             _ext.library().cfmoe_launch_stage(
                 _ext.STAGES.index(stage),
@@ -809,7 +830,7 @@ class ProgressiveReader:
                 _pointer(padding),
                 out.data_ptr(),
                 tokens,
-                self._charges,
+                None,
                 self._stream(),
             )
         )
@@ -819,7 +840,8 @@ class ProgressiveReader:
 
         Enqueued torch ops on the current stream (no host sync): the kept count
         varies per token, so charges follow progressive.py:2189-2225 with the
-        per-token selected counts.
+        per-token selected counts. The device adds the per-tile screen terms
+        (slots 11, 15) and, in grouped calls, the union rows (slot 12).
         """
         p = self.plan
         h, i, k, n, rank = (
@@ -854,10 +876,12 @@ class ProgressiveReader:
         work[7] += recovery
         work[9] += physical_selection
         work[10] += count * h
-        work[11] += physical_sketch
-        work[12] += 2 * 2 * h * done
+        if tokens >= self.grouped_tokens:
+            work[16] += count
+        else:
+            work[12] += 2 * 2 * h * done
         work[13] += 2 * h * kept
-        work[14] += 2 * rank * (candidates - kept)
+        work[14] += 2 * rank * candidates
         work[17] += physical_sketch
         work[19] += count
 
@@ -887,6 +911,8 @@ class ProgressiveReader:
         point = self.selection_score == "point"
         splits = _screen_splits(h)
         planes = 1 + (not point)
+        split_io = float(16 * splits * n * planes) * (splits > 1) * screened
+        split_adds = float(2 * (splits - 1) * n * planes) * screened
         return {
             "charged_bytes": charged,
             "reference_bytes": reference,
@@ -913,27 +939,36 @@ class ProgressiveReader:
             )
             * screened,
             "rotation_arithmetic_per_token": float(11 * h) * screened,
-            "grouped_rotation_input_io_bytes_per_token": 0.0,
-            "grouped_rotation_arithmetic_per_token": 0.0,
+            # one rotation launch serves every batch size
+            "grouped_rotation_input_io_bytes_per_token": float(
+                2 * h + ((12 if input_sparse else 8) * p.screen_coordinates + 8) * (h // 128)
+            )
+            * screened,
+            "grouped_rotation_arithmetic_per_token": float(11 * h) * screened,
             # The mask's cutoff is a 31-step binary search over magnitude bits
             # (two ballots per step) rather than a sort.
             "screen_ranking_compare_exchanges_per_token": float(h // 128 * 31 * 128)
             * input_sparse,
             "screen_mask_arithmetic_per_token": float(h // 128 * 9 * 128) * input_sparse,
             "screen_compaction_scan_adds_per_token": float(h // 128 * 127) * input_sparse,
-            "batch_one_screen_split_io_bytes": float(16 * splits * n * planes)
-            * (splits > 1) * screened,
-            "batched_screen_split_io_bytes_per_token": float(16 * splits * n * planes)
-            * (splits > 1) * screened,
-            "batched_screen_split_adds_per_token": float(2 * (splits - 1) * n * planes)
-            * screened,
+            # The one (expert-major) screen runs at every batch size: each
+            # split's FP32 partials are written and read back once; there are
+            # no arrival counters. Its workgroups stage the tile's kept grid
+            # values and coordinates (8 B each) once per range of row tiles,
+            # at most ceil(2 I / 64) ranges.
+            "batch_one_screen_split_io_bytes": split_io,
+            "batched_screen_split_io_bytes_per_token": split_io,
+            "batched_screen_split_adds_per_token": split_adds,
             "batch_one_screen_counter_io_bytes": 0.0,
             "batched_screen_counter_io_bytes_per_token": 0.0,
             "batch_one_screen_counter_sector_bytes_upper_bound": 0.0,
             "batched_screen_counter_sector_bytes_per_token_upper_bound": 0.0,
-            "grouped_screen_split_io_bytes_per_token": 0.0,
-            "grouped_screen_split_adds_per_token": 0.0,
-            "grouped_screen_union_io_bytes_per_token_upper_bound": 0.0,
+            "grouped_screen_split_io_bytes_per_token": split_io,
+            "grouped_screen_split_adds_per_token": split_adds,
+            "grouped_screen_union_io_bytes_per_token_upper_bound": float(
+                8 * k * (h // 128) * p.screen_coordinates * -(-2 * i // 64)
+            )
+            * screened,
             "per_token_screen_dot_terms": float(
                 k * 2 * i * (h // 128) * p.screen_coordinates
             )
@@ -948,7 +983,11 @@ class ProgressiveReader:
             "grouped_rows": grouped_rows,
             "grouped_issued_matrix_macs": grouped_macs,
             "workspace_bytes": float(self.workspace_bytes),
-            "batch_one_completion_shared_bytes_per_cta_upper_bound": 0.0,
+            # below the grouped size the exact launch stages encoder rows in LDS
+            "batch_one_completion_shared_bytes_per_cta_upper_bound": float(
+                4 * 64 * 2 * (-(-self.rank // 8) * 8 + 8)
+            )
+            * (self.rank > 0),
             "small_batch_recovery_counter_io_bytes_per_token": 0.0,
             "small_batch_recovery_counter_sector_bytes_per_token_upper_bound": 0.0,
             "small_batch_radix_scratch_io_bytes_per_token_upper_bound": 0.0,

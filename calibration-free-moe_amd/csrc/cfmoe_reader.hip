@@ -303,6 +303,9 @@ struct PrepareArgs {
   int32_t *pair_tiles;
   double *read_work;
   double charges[18];
+  // per tile of pairs: sketch bytes the screen streams, its matrix-core
+  // MACs, and (grouped dense plans) the gate/up bytes the exact rows read
+  double tile_sketch_bytes, tile_screen_macs, tile_row_bytes;
   int T, H, K, E, keep;
   uint32_t flags;
   int route, rotate, cells;
@@ -507,13 +510,21 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
     }
   }
   if (tid == 0) *a.group_total = total_tiles;
-  // fixed read charges: one add per slot for all active tokens (integers, exact)
+  // read statistics: one add per slot for all active tokens, then the
+  // per-tile terms (integers, exact in FP64)
   if (a.flags & CFMOE_ACCOUNT) {
     int active = 0;
     for (int t = tid; t < T; t += kPrepareThreads) active += is_active(a.padding, t);
     active = block_sum(active, scratch);
     if (tid < 18 && a.charges[tid] != 0.0 && active > 0)
       atomicAdd(a.read_work + tid, a.charges[tid] * static_cast<double>(active));
+    const double tiles = static_cast<double>(total_tiles);
+    if (tid == 32 && a.tile_sketch_bytes != 0.0 && total_tiles > 0)
+      atomicAdd(a.read_work + 11, tiles * a.tile_sketch_bytes);
+    if (tid == 33 && a.tile_screen_macs != 0.0 && total_tiles > 0)
+      atomicAdd(a.read_work + 15, tiles * a.tile_screen_macs);
+    if (tid == 34 && a.tile_row_bytes != 0.0 && total_tiles > 0)
+      atomicAdd(a.read_work + 12, tiles * a.tile_row_bytes);
   }
 }
 
@@ -1011,6 +1022,8 @@ struct SelectArgs {
   int32_t *starts;
   int32_t *tile_starts;
   int32_t *down_tile_starts;
+  double *read_work;  // slot 12 += union_row_bytes per (tile, channel) some pair kept (or NULL)
+  double union_row_bytes;
   int N, F, I, K;
   int thresholded;
 };
@@ -1131,6 +1144,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   const int packed = block_exclusive(above_here | (tied_here << 16), scratch, &packed_total);
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
   int above_before = packed & 0xffff, tied_before = packed >> 16;
+  int union_rows = 0;  // (tile, channel) words this thread turned nonzero
   // the slot of the current candidate and the next slot start at or after
   // this thread's first candidate (no division per key)
   int slot = first / a.I, next_slot = (first + a.I - 1) / a.I, boundary = next_slot * a.I;
@@ -1159,15 +1173,24 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
         a.next_ids[static_cast<long>(t) * a.F + position] = i;
         // the channel's bit for this pair in its tile's mask (OR: any order)
         const int slot_tile = a.tile_masks ? slot_tiles[slot] : -1;
-        if (slot_tile >= 0)
-          atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
-                   1u << (slot_tile % kGroupPairs));
+        if (slot_tile >= 0) {
+          const uint32_t before = atomicOr(
+              &a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
+              1u << (slot_tile % kGroupPairs));
+          union_rows += before == 0u;  // the first pair of its tile to keep the channel
+        }
       }
     }
   }
   for (int p = kept_total + tid; p < a.F; p += kSelectThreads)
     a.next_ids[static_cast<long>(t) * a.F + p] = -1;
   if (tid == 0) slot_start[a.K] = min(kept_total, a.F);
+  if (a.read_work) {
+    // each union row of the grouped exact rows is counted once, by the token
+    // whose select turned its word nonzero (one FP64 add per token)
+    const int rows = block_sum(union_rows, scratch);
+    if (tid == 0 && rows > 0) atomicAdd(a.read_work + 12, rows * a.union_row_bytes);
+  }
   __syncthreads();
   // wave 0: lane k writes slot k's count, start and tile starts (K <= 64)
   if (tid < kWave) {
@@ -1322,8 +1345,9 @@ __device__ __forceinline__ void encode_tile_direct(const Args &a, int tile, int 
       buffer_resource(a.partial + base + a.N, 4 * rows), 4 * lane, 0, 0));
   // the tile's rows of E (rows past I read zeros)
   const int r = lane & 31, half = lane >> 5;
+  // (an absent slot's resource is empty: its loads read zeros, request nothing)
   const __amdgpu_buffer_rsrc_t block = buffer_resource(
-      a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + tile * 64) * R, rows * R * 2);
+      a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + tile * 64) * R, local ? rows * R * 2 : 0);
   uint16_t coefficient[32];
 #pragma unroll
   for (int i = 0; i < 32; ++i)
@@ -1442,7 +1466,7 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
   }
 }
 
-// Grouped exact rows (batches of kGroupExactTokens or more, as
+// Grouped exact rows (batches of grouped_tokens or more, as
 // progressive.py:2655-2718): wave = (16-pair expert tile, channel). The
 // select kernel's tile mask names the tile's pairs that kept the channel; it
 // and the tile's pairs (16 slots per tile) are read together. If any pair
@@ -1862,7 +1886,6 @@ struct OutputArgs {
   int columns;  // outputs per workgroup (64 or 256, at most kOutputThreads)
 };
 
-constexpr int kGroupExactTokens = 16;  // batches that use group_exact_kernel
 constexpr int kOutputThreads = 512;
 constexpr int kMaxEncoderTiles = 16; // ceil(I / 64) at I <= 1024
 constexpr int kTileBatch = 8;        // tile partials loaded together per thread
@@ -2025,11 +2048,14 @@ int validate(const cfmoe_dims *d) {
   if (d->experts < 1 || d->experts > kMaxExperts) return fail(CFMOE_EINVAL, "experts must be in [1, 4096]");
   if (d->hidden > 128 * 8 * kMaxSpan) return fail(CFMOE_EINVAL, "hidden must be at most 2048");
   if (2 * d->width > kMaxRows) return fail(CFMOE_EINVAL, "width must be at most 1024");
+  if (d->grouped_tokens < 0) return fail(CFMOE_EINVAL, "grouped_tokens must be >= 0");
   return 0;
 }
 
+constexpr int kDefaultGroupedTokens = 16;  // cfmoe_dims.grouped_tokens = 0
+
 struct Shape {
-  int H, I, K, N, F, R, B, keep, splits, span, max_tiles, encoder_tiles;
+  int H, I, K, N, F, R, B, keep, splits, span, max_tiles, encoder_tiles, grouped_tokens;
   bool screened;
 };
 
@@ -2048,6 +2074,7 @@ Shape shape_of(const cfmoe_dims *d) {
   s.max_tiles = (s.F + kDownTile - 1) / kDownTile + s.K - 1;
   s.encoder_tiles = (s.I + 63) / 64;
   s.screened = s.F < s.N;
+  s.grouped_tokens = d->grouped_tokens > 0 ? d->grouped_tokens : kDefaultGroupedTokens;
   return s;
 }
 
@@ -2092,6 +2119,19 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.read_work = ws->read_work;
   if (charges && (d->flags & CFMOE_ACCOUNT))
     for (int i = 0; i < 18; ++i) a.charges[i] = charges[i];
+  if (route && (d->flags & CFMOE_ACCOUNT)) {
+    // per tile: the screen streams the expert's trit planes (64 I B bytes)
+    // and its FP16 scale (and residual) planes, and issues 2 I x 16 pairs x
+    // 128 coordinates x 3 grid digits int8 MACs per block; a grouped call of
+    // a dense plan reads every gate/up row of the tile's expert once
+    const bool gh5 = !(d->flags & CFMOE_POINT);
+    if (s.screened) {
+      a.tile_sketch_bytes = 64.0 * s.I * s.B + 2.0 * 2 * s.I * s.B * (gh5 ? 2 : 1);
+      a.tile_screen_macs = 2.0 * s.I * kGroupPairs * 128.0 * 3 * s.B;
+    } else if (tokens >= s.grouped_tokens) {
+      a.tile_row_bytes = 4.0 * s.H * s.I;
+    }
+  }
   a.T = tokens;
   a.H = s.H;
   a.K = s.K;
@@ -2255,10 +2295,15 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   sel.I = s.I;
   sel.K = s.K;
   sel.thresholded = (flags & CFMOE_THRESHOLD) != 0;
-  // per-(tile, channel) pair masks for the grouped exact kernel
-  const bool masked = s.screened && tokens >= kGroupExactTokens;
+  // per-(tile, channel) pair masks for the grouped exact kernel; the select
+  // kernel counts their nonzero words as the union rows the grouped exact
+  // launch reads (4 H bytes each)
+  const bool grouped = tokens >= s.grouped_tokens;
+  const bool masked = s.screened && grouped;
   sel.pair_tiles = workspace->pair_tiles;
   sel.tile_masks = masked ? workspace->tile_masks : nullptr;
+  sel.read_work = masked && (flags & CFMOE_ACCOUNT) ? workspace->read_work : nullptr;
+  sel.union_row_bytes = 4.0 * s.H;
 
   if (s.screened) {
     GroupScreenArgs sc;
@@ -2367,7 +2412,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   // launch fewer); grouped batches run it in the grouped exact launch when it
   // needs no LDS (R = kDirectRank; the LDS encoder's dynamic LDS would apply to
   // every exact workgroup and halve their occupancy)
-  const bool small = tokens < kGroupExactTokens;
+  const bool small = !grouped;
   // grouped batches: the exact stage builds the down kernel's workgroup order
   // (expert-grouped per XCD) and the down stage reads it
   const bool down_order = !small;
@@ -2395,7 +2440,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   ex.F = s.F;
   ex.gelu = gelu;
   if (stages & (1u << CFMOE_STAGE_EXACT)) {
-    if (tokens >= kGroupExactTokens) {
+    if (grouped) {
       GroupExactArgs gx;
       gx.gate_up = ex.gate_up;
       gx.x = ex.x;
@@ -2499,7 +2544,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.R = s.R;
   op.max_tiles = s.max_tiles;
   op.encoder_tiles = s.encoder_tiles;
-  op.columns = tokens >= kGroupExactTokens && s.K <= 16 ? 256 : 64;  // LDS <= 16 KB
+  op.columns = grouped && s.K <= 16 ? 256 : 64;  // LDS <= 16 KB
   hipLaunchKernelGGL(output_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
                      dim3(kOutputThreads), static_cast<unsigned>(s.K * op.columns * sizeof(float)),
                      stream, op);

@@ -36,14 +36,14 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 5
+#define CFMOE_ABI_VERSION 6
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
 #define CFMOE_GELU 2u           /* tanh-GELU gate activation (else SiLU) */
 #define CFMOE_GEOMETRY 4u       /* recovery geometry (alpha, beta) is read */
 #define CFMOE_THRESHOLD 8u      /* keep scores >= *threshold, at most F */
-#define CFMOE_ACCOUNT 16u       /* add fixed per-token read charges */
+#define CFMOE_ACCOUNT 16u       /* add the call's read statistics to read_work */
 #define CFMOE_IDS_INT64 32u     /* router ids are int64 (else int32) */
 #define CFMOE_WEIGHTS_BF16 64u  /* router weights are bf16 (else fp32) */
 #define CFMOE_INPUT_PREPARED 128u /* cfmoe_prepare_input already rotated */
@@ -74,6 +74,9 @@ typedef struct cfmoe_dims {
   int32_t final_count; /* F, channels kept per token */
   int32_t keep;        /* rotated coordinates kept per 128-block (1..128) */
   uint32_t flags;
+  int32_t grouped_tokens; /* calls of at least this many tokens compute the kept
+                             channels expert-major (one read of each union row
+                             per tile of <= 16 pairs); 0 = the default, 16 */
 } cfmoe_dims;
 
 /* Resident per-layer tensors. The reader borrows them; none is written. */
@@ -142,8 +145,12 @@ CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, in
 /* One reader call: routed-expert output of `tokens` rows (progressive.py:
  * 3876-4472). hidden bf16 [T, H]; router_ids [T, K] int32/int64; router
  * weights [T, K] fp32/bf16; padding uint8 [T] or NULL; out bf16 [T, H].
- * charges: 18 doubles added to read_work[0..17] per active token when
- * CFMOE_ACCOUNT is set (progressive.py:4492-4524), else ignored. */
+ * With CFMOE_ACCOUNT set the call adds its read statistics to read_work
+ * (progressive.py:3507-3515, :4492-4524, :2114-2317): charges[0..17] times
+ * the active tokens, plus what the device counts itself -- the sketch bytes
+ * the screen streams and its matrix-core MACs per tile of pairs (slots 11,
+ * 15) and, for grouped calls, the gate/up rows of each tile's union of kept
+ * channels (slot 12). charges may be NULL (no per-token terms). */
 CFMOE_API int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights,
                   const cfmoe_workspace *workspace, const void *hidden,
                   const void *router_ids, const void *router_weights,

@@ -44,7 +44,12 @@
  *    correction = bf16(fma chain over r of U[o, r] * bf16(latent_r));
  *    out = bf16(routed + correction).
  *
- * Build: see oracle/Makefile (-O2 -ffp-contract=off, no fast-math).
+ * Build: see oracle/Makefile (-O2 -ffp-contract=off, no fast-math, OpenMP).
+ *
+ * Threads: the `threads` argument of the heavy stages splits independent
+ * outputs (rows, kept channels, output columns, candidates) over OpenMP
+ * threads; every output is still computed by one thread in the order above,
+ * so the results do not depend on the thread count.
  */
 #include <math.h>
 #include <stdint.h>
@@ -295,43 +300,37 @@ void orc_rotate(int T, int H, int keep, const uint16_t *x, const int8_t *signs,
 void orc_screen(int T, int H, int I, int K, int keep, const uint8_t *codes,
                 const uint16_t *stats, const int32_t *coords, const int32_t *qvals,
                 const int32_t *qexp, const float *norm2, const int32_t *ids,
-                const uint8_t *padding, float *partial, float *variances) {
+                const uint8_t *padding, float *partial, float *variances, int threads) {
   int B = H / 128, N = K * I, rows = 2 * I;
   int stride = orc_code_stride(rows);
   long storage = orc_storage_bytes(rows, H);
   int splits = B < 8 ? B : 8;
   int span = (B + splits - 1) / splits;
-  int64_t *sums = malloc(sizeof(int64_t) * rows);
-  float *dots = malloc(sizeof(float) * (size_t)B * rows);
   for (int t = 0; t < T; ++t) {
     int active = padding ? !padding[t] : 1;
     for (int k = 0; k < K; ++k) {
       int e = ids[t * K + k];
       int local = active && e >= 0;
       const uint8_t *ec = local ? codes + (long)e * storage : NULL;
-      for (int b = 0; b < B; ++b) {
-        long cell = (long)t * B + b;
-        memset(sums, 0, sizeof(int64_t) * rows);
-        if (local) {
-          for (int p = 0; p < keep; ++p) {
-            int coord = keep >= 128 ? p : coords[cell * keep + p];
-            int64_t q = qvals[cell * keep + p];
-            for (int r = 0; r < rows; ++r)
-              sums[r] += (int64_t)decode_trit(ec, I, B, stride, r, b, coord) * q;
-          }
-        }
-        for (int r = 0; r < rows; ++r)
-          dots[(long)b * rows + r] = ldexpf((float)(int32_t)sums[r], -qexp[cell]);
-      }
+#pragma omp parallel for schedule(static) num_threads(threads)
       for (int r = 0; r < rows; ++r) {
         float estimate = 0.0f, variance = 0.0f;
         for (int s = 0; s < splits; ++s) {
           float part = 0.0f, vpart = 0.0f;
           for (int b = s * span; b < (s + 1) * span && b < B; ++b) {
+            long cell = (long)t * B + b;
+            /* exact integer block dot on the grid, then one rounding */
+            int64_t sum = 0;
+            if (local)
+              for (int p = 0; p < keep; ++p) {
+                int coord = keep >= 128 ? p : coords[cell * keep + p];
+                sum += (int64_t)decode_trit(ec, I, B, stride, r, b, coord) * qvals[cell * keep + p];
+              }
+            float dot = ldexpf((float)(int32_t)sum, -qexp[cell]);
             if (local) {
               const uint16_t *plane = stats + (((long)e * B + b) * 2) * rows;
-              part = fmaf(dots[(long)b * rows + r], half_to_float(plane[r]), part);
-              vpart = fmaf(half_to_float(plane[rows + r]), norm2[(long)t * B + b], vpart);
+              part = fmaf(dot, half_to_float(plane[r]), part);
+              vpart = fmaf(half_to_float(plane[rows + r]), norm2[cell], vpart);
             }
           }
           estimate = s == 0 ? part : estimate + part;
@@ -344,8 +343,6 @@ void orc_screen(int T, int H, int I, int K, int keep, const uint8_t *codes,
       }
     }
   }
-  free(sums);
-  free(dots);
 }
 
 /* ------------------------------------------------------------------ */
@@ -507,15 +504,16 @@ float orc_row_dot(int H, const uint16_t *row, const uint16_t *x) {
 void orc_exact(int T, int H, int I, int K, int F, const uint16_t *gate_up,
                const uint16_t *x, const int32_t *ids, const uint8_t *padding,
                const int32_t *next_ids, int gelu, float *partial,
-               uint16_t *activations, uint8_t *completed) {
+               uint16_t *activations, uint8_t *completed, int threads) {
   int N = K * I;
   uint16_t *zero = calloc((size_t)H, sizeof(uint16_t));
   for (int t = 0; t < T; ++t) {
     int active = padding ? !padding[t] : 1;
     memset(completed + (long)t * N, 0, N);
+#pragma omp parallel for schedule(dynamic, 16) num_threads(threads)
     for (int f = 0; f < F; ++f) {
       int logical = next_ids[(long)t * F + f];
-      if (logical < 0) break;
+      if (logical < 0) continue; /* the -1 padding of a thresholded list */
       int k = logical / I, c = logical % I;
       int e = ids[t * K + k];
       float g = 0.0f, u = 0.0f;
@@ -542,35 +540,38 @@ void orc_exact(int T, int H, int I, int K, int F, const uint16_t *gate_up,
 void orc_down(int T, int H, int I, int K, int F, const uint16_t *down,
               const uint16_t *activations, const int32_t *ids, const uint8_t *padding,
               const int32_t *next_ids, const int32_t *counts, const int32_t *starts,
-              float *values) {
+              float *values, int threads) {
   int N = K * I;
-  float *total = malloc(sizeof(float) * H);
-  float *tile = malloc(sizeof(float) * H);
   for (int t = 0; t < T; ++t) {
     int active = padding ? !padding[t] : 1;
     for (int k = 0; k < K; ++k) {
       int e = ids[t * K + k];
       int count = counts[t * K + k], start = starts[t * K + k];
-      for (int o = 0; o < H; ++o) total[o] = 0.0f;
-      for (int begin = 0; begin < count; begin += DOWN_TILE) {
-        for (int o = 0; o < H; ++o) tile[o] = 0.0f;
-        for (int j = begin; j < begin + DOWN_TILE && j < count; ++j) {
-          int logical = next_ids[(long)t * F + start + j];
-          int c = logical % I;
-          float a = bf16_to_float(activations[(long)t * N + logical]);
-          const uint16_t *row = down + ((long)e * I + c) * H;
-          for (int o = 0; o < H; ++o) {
-            float d = (active && e >= 0) ? bf16_to_float(row[o]) : 0.0f;
-            tile[o] = fmaf(d, a, tile[o]);
+      /* output columns in chunks of 64, one thread each */
+#pragma omp parallel for schedule(static) num_threads(threads)
+      for (int o0 = 0; o0 < H; o0 += 64) {
+        int o1 = o0 + 64 < H ? o0 + 64 : H;
+        float total[64], tile[64];
+        for (int o = o0; o < o1; ++o) total[o - o0] = 0.0f;
+        for (int begin = 0; begin < count; begin += DOWN_TILE) {
+          for (int o = o0; o < o1; ++o) tile[o - o0] = 0.0f;
+          for (int j = begin; j < begin + DOWN_TILE && j < count; ++j) {
+            int logical = next_ids[(long)t * F + start + j];
+            int c = logical % I;
+            float a = bf16_to_float(activations[(long)t * N + logical]);
+            const uint16_t *row = down + ((long)e * I + c) * H;
+            for (int o = o0; o < o1; ++o) {
+              float d = (active && e >= 0) ? bf16_to_float(row[o]) : 0.0f;
+              tile[o - o0] = fmaf(d, a, tile[o - o0]);
+            }
           }
+          for (int o = o0; o < o1; ++o)
+            total[o - o0] = begin == 0 ? tile[o - o0] : total[o - o0] + tile[o - o0];
         }
-        for (int o = 0; o < H; ++o) total[o] = begin == 0 ? tile[o] : total[o] + tile[o];
+        for (int o = o0; o < o1; ++o) values[((long)t * K + k) * H + o] = bf16_round(total[o - o0]);
       }
-      for (int o = 0; o < H; ++o) values[((long)t * K + k) * H + o] = bf16_round(total[o]);
     }
   }
-  free(total);
-  free(tile);
 }
 
 /* ------------------------------------------------------------------ */

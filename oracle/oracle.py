@@ -136,8 +136,12 @@ class Weights:
 
 def forward(w: Weights, x_bits, router_ids, router_weights, *, final_count: int,
             keep: int, padding=None, point: bool = True, gelu: bool = False,
-            threshold: float | None = None) -> dict[str, np.ndarray]:
-    """Run the whole reader for one call; returns every intermediate."""
+            threshold: float | None = None, threads: int = 1) -> dict[str, np.ndarray]:
+    """Run the whole reader for one call; returns every intermediate.
+
+    `threads` OpenMP threads split the screen's rows, the kept channels and
+    the down outputs (the results do not depend on it).
+    """
     L = lib()
     T, H = x_bits.shape
     E, rows, _ = w.gate_up.shape
@@ -153,7 +157,8 @@ def forward(w: Weights, x_bits, router_ids, router_weights, *, final_count: int,
     screened = F < N
     if screened:
         L.orc_screen(T, H, I, K, keep, _p(w.codes), _p(w.stats), _p(coords), _p(qvals),
-                     _p(qexp), _p(norm2), _p(ids), _p(pad), _p(partial), _p(variances))
+                     _p(qexp), _p(norm2), _p(ids), _p(pad), _p(partial), _p(variances),
+                     int(threads))
     scores = np.zeros((T, N), np.float32)
     next_ids = np.empty((T, F), np.int32)
     selected = np.zeros((T, N), np.uint8)
@@ -176,10 +181,10 @@ def forward(w: Weights, x_bits, router_ids, router_weights, *, final_count: int,
     completed = np.zeros((T, N), np.uint8)
     xb = np.ascontiguousarray(x_bits, dtype=np.uint16)
     L.orc_exact(T, H, I, K, F, _p(w.gate_up), _p(xb), _p(ids), _p(pad), _p(next_ids),
-                int(gelu), _p(partial), _p(activations), _p(completed))
+                int(gelu), _p(partial), _p(activations), _p(completed), int(threads))
     values = np.empty((T, K, H), np.float32)
     L.orc_down(T, H, I, K, F, _p(w.down), _p(activations), _p(ids), _p(pad),
-               _p(next_ids), _p(counts), _p(starts), _p(values))
+               _p(next_ids), _p(counts), _p(starts), _p(values), int(threads))
     latent = np.zeros((T, max(R, 1)), np.float32)
     if R:
         L.orc_encode(T, I, K, R, _p(w.encoder_t), _p(partial), _p(activations),

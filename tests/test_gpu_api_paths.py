@@ -104,3 +104,45 @@ def test_fine_grained_experts_batch_1(keep):
     assert_parity(reader, out, expected, 1)
     assert int(reader.selected[0].sum()) == plan.final_count
     np.testing.assert_array_equal(expected["counts"].sum(1), plan.final_count)
+
+
+def test_grouped_and_per_token_calls_agree_and_report_their_reads():
+    """The same batch through per-token exact rows (grouped_tokens above the
+    batch) and grouped ones (grouped_tokens = 2): identical results, identical
+    read cost, and the requested bytes each kernel set reads (reference closed
+    forms, tests/test_progressive_reader.py:959-978)."""
+    tokens, experts, top_k, hidden, width, rank = 24, 16, 4, 512, 256, 16
+    layer = make_layer(hidden=hidden, width=width, experts=experts, top_k=top_k, rank=rank,
+                       tokens=tokens, seed=106)
+    plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=top_k,
+                          retention=0.123, screen_keep=0.625)
+    per_token = build(layer, plan, tokens, selection_score="point", grouped_tokens=tokens + 1)
+    grouped = build(layer, plan, tokens, selection_score="point", grouped_tokens=2)
+    hidden_rows = layer.hidden.to(DEVICE)
+    ids, weights = layer.ids.to(DEVICE), layer.weights.to(DEVICE)
+    padding = torch.tensor([t % 7 == 3 for t in range(tokens)], device=DEVICE)
+    active = int((~padding).sum())
+    a = per_token(hidden_rows, ids, weights, padding)
+    b = grouped(hidden_rows, ids, weights, padding)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    assert torch.equal(per_token.selected[:tokens], grouped.selected[:tokens])
+    token_report, grouped_report = per_token.report(), grouped.report()
+    for key in ("charged_bytes", "logical_charged_bytes", "reference_bytes"):
+        assert token_report[key] == grouped_report[key]
+    assert grouped_report["grouped_rows"] == active and token_report["grouped_rows"] == 0
+    # gate/up: every kept channel per token, or each tile's union once
+    ws = grouped.workspace
+    tiles = int(ws.group_total.item())
+    masks = ws.tile_masks[: tiles * width].cpu().numpy().view(np.uint32)
+    assert token_report["issued_gate_up_bytes"] == 4 * hidden * plan.final_count * active
+    assert grouped_report["issued_gate_up_bytes"] == 4 * hidden * int((masks != 0).sum())
+    assert grouped_report["issued_gate_up_bytes"] < token_report["issued_gate_up_bytes"]
+    # down and encoder rows are requested per token in both
+    for report in (token_report, grouped_report):
+        assert report["issued_down_bytes"] == 2 * hidden * plan.final_count * active
+        assert report["issued_recovery_encoder_bytes"] == 2 * rank * top_k * width * active
+        # the screen streams each tile's trit planes and FP16 scales once
+        blocks = hidden // 128
+        assert report["issued_sketch_bytes"] == tiles * (64 * width * blocks + 4 * width * blocks)
+        assert report["grouped_issued_matrix_macs"] == tiles * 2 * width * 16 * 128 * 3 * blocks

@@ -548,3 +548,15 @@ def test_token_parallel_oracle_equals_one_call():
     assert whole.keys() == split.keys()
     for key in whole:
         assert np.array_equal(whole[key], split[key]), key
+
+
+def test_thread_count_does_not_change_results():
+    layer = small_layer(tokens=2, seed=37)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    args = (cpu_weights(layer, point=False), bits(layer.hidden), layer.ids.numpy(),
+            layer.weights.numpy())
+    one = oracle.forward(*args, final_count=plan.final_count, keep=80, point=False)
+    many = oracle.forward(*args, final_count=plan.final_count, keep=80, point=False, threads=5)
+    for key in one:
+        assert np.array_equal(one[key], many[key]), key
