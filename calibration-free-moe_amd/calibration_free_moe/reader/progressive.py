@@ -679,6 +679,18 @@ class ProgressiveReader:
             flags |= _ext.INPUT_PREPARED
         return flags
 
+    def _call_dims(self, ids: Tensor, weights: Tensor, input_prepared: bool) -> _ext.Dims:
+        """C dimensions and flags of one call with these router outputs."""
+        p = self.plan
+        screened = p.completion_count < p.candidate_count
+        return _dims(
+            p,
+            self.native_gu.shape[0],
+            self.rank,
+            self._flags(ids, weights, input_prepared and screened),
+            self.grouped_tokens,
+        )
+
     def _validate_input(self, hidden: Tensor, padding: Tensor | None) -> int:
         """Check the hidden rows and padding mask; return the token count."""
         tokens = hidden.shape[0]
@@ -773,14 +785,7 @@ class ProgressiveReader:
             raise ValueError("Sparse input exceeds the prepared token/candidate contract")
         if out is None:
             out = torch.empty_like(hidden)
-        screened = p.completion_count < p.candidate_count
-        dims = _dims(
-            p,
-            self.native_gu.shape[0],
-            self.rank,
-            self._flags(ids, weights, input_prepared and screened),
-            self.grouped_tokens,
-        )
+        dims = self._call_dims(ids, weights, input_prepared)
         _ext.check(
             _ext.library().cfmoe_forward(
                 ctypes.byref(dims),

@@ -1072,6 +1072,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int slot_start[65];
   __shared__ int slot_tiles[64];
   __shared__ int shared_bin, shared_above;
+  __shared__ int union_scratch[kSelectThreads / kWave];
   const int t = blockIdx.x, tid = threadIdx.x;
   if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
   for (int i = tid; i < 3 * kSelectSlots; i += kSelectThreads) (&histogram[0][0])[i] = 0;
@@ -1185,13 +1186,19 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   for (int p = kept_total + tid; p < a.F; p += kSelectThreads)
     a.next_ids[static_cast<long>(t) * a.F + p] = -1;
   if (tid == 0) slot_start[a.K] = min(kept_total, a.F);
+  // each union row of the grouped exact rows is counted once, by the token
+  // whose select turned its word nonzero: per-wave sums meet at the barrier
+  // below, wave 0 adds them (one FP64 add per token)
   if (a.read_work) {
-    // each union row of the grouped exact rows is counted once, by the token
-    // whose select turned its word nonzero (one FP64 add per token)
-    const int rows = block_sum(union_rows, scratch);
-    if (tid == 0 && rows > 0) atomicAdd(a.read_work + 12, rows * a.union_row_bytes);
+    const int rows = wave_sum_all(union_rows);
+    if ((tid & 63) == 0) union_scratch[tid >> 6] = rows;
   }
   __syncthreads();
+  if (a.read_work && tid == 0) {
+    int rows = 0;
+    for (int w = 0; w < kSelectThreads / kWave; ++w) rows += union_scratch[w];
+    if (rows > 0) atomicAdd(a.read_work + 12, rows * a.union_row_bytes);
+  }
   // wave 0: lane k writes slot k's count, start and tile starts (K <= 64)
   if (tid < kWave) {
     const bool slot = tid < a.K;
@@ -2577,3 +2584,4 @@ int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weight
 }
 
 }  // extern "C"
+
