@@ -24,6 +24,7 @@
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <pthread.h>
 #include <string.h>
 
 #include <algorithm>
@@ -2585,3 +2586,128 @@ int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weight
 
 }  // extern "C"
 
+// ---------------------------------------------------------------------------
+// Allocation-free forward: the workspace lives in one file-scope device array.
+//
+// For callers that cannot allocate device memory (code under graph capture,
+// tight serving loops, hosts that forbid hipMalloc). Every GPU the library
+// runs on holds its own copy of `scratch` until the process ends. In host code
+// the array's name is only a stand-in for the symbol: its device address on
+// the current GPU comes from hipGetSymbolAddress, looked up once per device
+// and kept in g_scratch_address; only that address is handed to kernels.
+
+namespace cfmoe {
+
+constexpr long kScratchBytes = 64L << 20;  // the largest workspace it carves
+constexpr long kScratchAlign = 256;        // every carved buffer starts on 256 B
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+pthread_mutex_t g_scratch_mutex = PTHREAD_MUTEX_INITIALIZER;
+void *g_scratch_address[kMaxDevices] = {};
+
+// Bytes of the workspace for `tokens` tokens, each buffer rounded up to
+// kScratchAlign; sizes[] receives the unrounded sizes.
+long carved_bytes(const cfmoe_dims *dims, int tokens, int64_t *sizes) {
+  cfmoe_workspace_sizes(dims, tokens, sizes, kWorkspaceBuffers);
+  long total = 0;
+  for (int i = 0; i < kWorkspaceBuffers; ++i)
+    total += (sizes[i] + kScratchAlign - 1) / kScratchAlign * kScratchAlign;
+  return total;
+}
+
+// The device address of `scratch` on `device` (the current device).
+int scratch_address(int device, unsigned char **address) {
+  if (device < 0 || device >= kMaxDevices) return fail(CFMOE_EINVAL, "device index out of range");
+  pthread_mutex_lock(&g_scratch_mutex);
+  int rc = 0;
+  if (!g_scratch_address[device]) {
+    void *found = nullptr;
+    const hipError_t status = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    if (status != hipSuccess || !found) {
+      snprintf(g_error, sizeof(g_error), "hipGetSymbolAddress(scratch) failed: %s",
+               hipGetErrorString(status));
+      rc = CFMOE_EHIP;
+    } else {
+      g_scratch_address[device] = found;
+    }
+  }
+  if (!rc) *address = static_cast<unsigned char *>(g_scratch_address[device]);
+  pthread_mutex_unlock(&g_scratch_mutex);
+  return rc;
+}
+
+}  // namespace cfmoe
+
+extern "C" {
+
+using namespace cfmoe;
+
+int64_t cfmoe_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int cfmoe_forward_noalloc(const cfmoe_dims *dims, const cfmoe_weights *weights,
+                          const void *hidden, const void *router_ids,
+                          const void *router_weights, const uint8_t *padding, void *out,
+                          int32_t tokens, double *read_work, const double *charges,
+                          cfmoe_stream stream) {
+  if (int rc = validate(dims)) return rc;
+  if (tokens < 1) return fail(CFMOE_EINVAL, "tokens out of range");
+  if ((dims->flags & CFMOE_ACCOUNT) && !read_work)
+    return fail(CFMOE_EINVAL, "CFMOE_ACCOUNT needs read_work");
+  // the size check is host arithmetic only: nothing is touched on a device
+  int64_t sizes[kWorkspaceBuffers];
+  const long need = carved_bytes(dims, tokens, sizes);
+  if (need > kScratchBytes) {
+    snprintf(g_error, sizeof(g_error),
+             "the call needs %ld workspace bytes; the allocation-free entry point holds %ld "
+             "(use cfmoe_forward with a caller workspace)",
+             need, kScratchBytes);
+    return CFMOE_EINVAL;
+  }
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(CFMOE_EHIP, "hipGetDevice failed");
+  if (stream) {
+    hipDevice_t stream_device = 0;
+    if (hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &stream_device) != hipSuccess)
+      return fail(CFMOE_EHIP, "hipStreamGetDevice failed");
+    if (stream_device != device)
+      return fail(CFMOE_EINVAL, "the stream is not on the current device");
+  }
+  unsigned char *base = nullptr;
+  if (int rc = scratch_address(device, &base)) return rc;
+  // carve the buffers in struct order
+  cfmoe_workspace ws;
+  memset(&ws, 0, sizeof(ws));
+  ws.capacity = tokens;
+  void **slots[kWorkspaceBuffers] = {
+      reinterpret_cast<void **>(&ws.ids), reinterpret_cast<void **>(&ws.weights),
+      reinterpret_cast<void **>(&ws.planes), reinterpret_cast<void **>(&ws.coordinates),
+      reinterpret_cast<void **>(&ws.qvals), reinterpret_cast<void **>(&ws.qexp),
+      reinterpret_cast<void **>(&ws.qsums), reinterpret_cast<void **>(&ws.norm2),
+      reinterpret_cast<void **>(&ws.partial), reinterpret_cast<void **>(&ws.variances),
+      reinterpret_cast<void **>(&ws.screen_parts),
+      reinterpret_cast<void **>(&ws.screen_variance_parts),
+      reinterpret_cast<void **>(&ws.scores), reinterpret_cast<void **>(&ws.next_ids),
+      reinterpret_cast<void **>(&ws.selected), reinterpret_cast<void **>(&ws.completed),
+      reinterpret_cast<void **>(&ws.activations), reinterpret_cast<void **>(&ws.starts),
+      reinterpret_cast<void **>(&ws.counts), reinterpret_cast<void **>(&ws.tile_starts),
+      reinterpret_cast<void **>(&ws.down_tile_starts),
+      reinterpret_cast<void **>(&ws.down_parts), reinterpret_cast<void **>(&ws.encoder_parts),
+      reinterpret_cast<void **>(&ws.latent), reinterpret_cast<void **>(&ws.group_experts),
+      reinterpret_cast<void **>(&ws.group_starts), reinterpret_cast<void **>(&ws.group_counts),
+      reinterpret_cast<void **>(&ws.group_pairs), reinterpret_cast<void **>(&ws.group_total),
+      reinterpret_cast<void **>(&ws.pair_tiles), reinterpret_cast<void **>(&ws.tile_masks),
+      reinterpret_cast<void **>(&ws.down_order),
+  };
+  long offset = 0;
+  for (int i = 0; i < kWorkspaceBuffers; ++i) {
+    *slots[i] = sizes[i] > 0 ? static_cast<void *>(base + offset) : nullptr;
+    offset += (sizes[i] + kScratchAlign - 1) / kScratchAlign * kScratchAlign;
+  }
+  ws.read_work = read_work;
+  return run_stages(~0u, dims, weights, &ws, hidden, router_ids, router_weights, padding, out,
+                    tokens, charges, stream);
+}
+
+}  // extern "C"

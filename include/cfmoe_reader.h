@@ -202,6 +202,25 @@ CFMOE_API int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *w
                         const cfmoe_workspace *workspace, const void *hidden,
                         const uint8_t *padding, int32_t tokens, cfmoe_stream stream);
 
+/* Allocation-free variant of cfmoe_forward. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP-graph
+ * capture, tight serving loops, hosts that forbid hipMalloc). Same arguments
+ * as cfmoe_forward minus the workspace, plus the caller's read_work [20]
+ * (needed only with CFMOE_ACCOUNT). The workspace is carved from one static
+ * device array of cfmoe_noalloc_scratch_bytes() bytes (64 MiB) that each GPU
+ * holds until the process ends; a call needing more returns CFMOE_EINVAL
+ * without touching the device. It calls no allocating routine. Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (several
+ * streams or threads) race. The stream must belong to the current device. */
+CFMOE_API int cfmoe_forward_noalloc(const cfmoe_dims *dims, const cfmoe_weights *weights,
+                                    const void *hidden, const void *router_ids,
+                                    const void *router_weights, const uint8_t *padding,
+                                    void *out, int32_t tokens, double *read_work,
+                                    const double *charges, cfmoe_stream stream);
+
+/* Bytes of the static device array behind cfmoe_forward_noalloc. */
+CFMOE_API int64_t cfmoe_noalloc_scratch_bytes(void);
+
 /* Thread-local message of the last failing call. */
 CFMOE_API const char *cfmoe_last_error(void);
 
