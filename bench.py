@@ -181,9 +181,12 @@ def stage_bytes(stage: str, tokens: int, rank: int) -> tuple[str, ...]:
 
 
 def stage_kernel(stage: str, tokens: int) -> str:
-    """Name of the kernel a stage launches at this batch size."""
+    """Name of the kernel a stage launches at this batch size (grouped
+    batches: the screen launch also scores, the score stage launches nothing)."""
     if stage == "exact" and tokens >= GROUP_EXACT_TOKENS:
         return "group_exact_kernel"
+    if stage == "screen" and tokens >= GROUP_EXACT_TOKENS:
+        return "fused_screen_kernel"
     return STAGE_KERNELS[stage]
 
 
@@ -494,7 +497,8 @@ def _rocprof_rows(directory: str, suffix: str) -> list[dict]:
 def summarize_trace(directory: str, command: str) -> str:
     """Per-kernel launch statistics of a rocprofv3 --kernel-trace --stats run."""
     durations: dict[str, list[int]] = {}
-    reader_kernels = set(STAGE_KERNELS.values()) | {"select_all_kernel", "group_exact_kernel"}
+    reader_kernels = set(STAGE_KERNELS.values()) | {"select_all_kernel", "group_exact_kernel",
+                                                     "fused_screen_kernel"}
     for row in _rocprof_rows(directory, "kernel_trace.csv"):
         name = _short_name(row["Kernel_Name"])
         if name not in reader_kernels:

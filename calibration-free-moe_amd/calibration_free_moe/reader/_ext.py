@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 POINT = 1
 GELU = 2
@@ -94,6 +94,7 @@ WORKSPACE_FIELDS = (
     ("pair_tiles", "int32"),
     ("tile_masks", "int32"),
     ("down_order", "int32"),
+    ("digits", "int8"),
 )
 
 

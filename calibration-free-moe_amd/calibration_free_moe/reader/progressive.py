@@ -189,7 +189,7 @@ class ReaderWorkspace:
         self._sizes = dict(zip((name for name, _ in _ext.WORKSPACE_FIELDS), sizes))
         dtype = {
             "int32": torch.int32, "float32": torch.float32, "bool": torch.bool,
-            "bfloat16": torch.bfloat16,
+            "bfloat16": torch.bfloat16, "int8": torch.int8,
         }
 
         def buffer(name: str, shape: tuple[int, ...]) -> Tensor:
@@ -250,6 +250,8 @@ class ReaderWorkspace:
         self.tile_masks = buffer("tile_masks", (capacity * n,))
         # Down workgroups' items grouped by expert per XCD, and their builders' records.
         self.down_order = buffer("down_order", (self._sizes["down_order"] // 4,))
+        # the kept grid values' three 8-bit digits per rotated coordinate
+        self.sketch_digits = buffer("digits", (capacity, blocks, 3, 128))
         # The reference's last-arrival counters; these kernels need none but the
         # attributes stay (all zero) for callers that inspect them.
         self.screen_counters = torch.zeros(
@@ -284,6 +286,7 @@ class ReaderWorkspace:
             self.down_tile_starts, self.down_parts, self.encoder_parts, self.latent,
             self.group_experts, self.group_starts, self.group_counts, self.group_pairs,
             self.group_total, self.pair_tiles, self.tile_masks, self.down_order,
+            self.sketch_digits,
         )
         self.bytes = sum(t.numel() * t.element_size() for t in buffers)
         self.charged = False
@@ -330,6 +333,7 @@ _WORKSPACE_ATTRS = (
     ("pair_tiles", "pair_tiles"),
     ("tile_masks", "tile_masks"),
     ("down_order", "down_order"),
+    ("digits", "sketch_digits"),
 )
 
 

@@ -282,6 +282,15 @@ __device__ int block_exclusive(int v, int *scratch, int *total) {
 // deterministic lists, no atomics in the order) and adds the fixed read
 // charges. Wave w of cell block i rotates cell 4 i + w = (token, block).
 
+// Balanced 8-bit digits of a grid value: q = d0 + 2^8 d1 + 2^16 d2 with
+// d_i in [-128, 127] (|q| <= 2^20).
+__device__ __forceinline__ void grid_digits(int q, int &d0, int &d1, int &d2) {
+  d0 = ((q + 128) & 255) - 128;
+  const int rest = (q - d0) >> 8;
+  d1 = ((rest + 128) & 255) - 128;
+  d2 = (rest - d1) >> 8;
+}
+
 struct PrepareArgs {
   const uint16_t *x;
   const int8_t *signs;
@@ -296,6 +305,7 @@ struct PrepareArgs {
   int32_t *qexp;
   int32_t *qsums;
   float *norm2;
+  int8_t *digits;  // [T, B, 3, 128] digit planes of the cell's grid values
   int32_t *group_experts;
   int32_t *group_starts;
   int32_t *group_counts;
@@ -313,7 +323,7 @@ struct PrepareArgs {
 };
 
 constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
-constexpr int kWorkspaceBuffers = 32;  // cfmoe_workspace pointers after capacity
+constexpr int kWorkspaceBuffers = 33;  // cfmoe_workspace pointers after capacity
 constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
@@ -636,6 +646,19 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
     a.qvals[cell * keep + pos1] = q1;
     if (keep < 128) a.coords[cell * keep + pos1] = 64 + lane;
   }
+  // the dense digit planes the screen stages (zero where not kept: q = 0)
+  {
+    int8_t *row = a.digits + cell * 3 * 128;
+    int d0, d1, d2;
+    grid_digits(q0, d0, d1, d2);
+    row[lane] = static_cast<int8_t>(d0);
+    row[128 + lane] = static_cast<int8_t>(d1);
+    row[256 + lane] = static_cast<int8_t>(d2);
+    grid_digits(q1, d0, d1, d2);
+    row[64 + lane] = static_cast<int8_t>(d0);
+    row[192 + lane] = static_cast<int8_t>(d1);
+    row[320 + lane] = static_cast<int8_t>(d2);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -702,13 +725,6 @@ __global__ __launch_bounds__(256) void pack_trit_planes_kernel(PackArgs a) {
       word[h] |= digit << (8 * (k % 4) + 2 * (k / 4));
     }
   a.planes[index] = make_uint2(word[0], word[1]);
-}
-
-__device__ __forceinline__ void grid_digits(int q, int &d0, int &d1, int &d2) {
-  d0 = ((q + 128) & 255) - 128;
-  const int rest = (q - d0) >> 8;
-  d1 = ((rest + 128) & 255) - 128;
-  d2 = (rest - d1) >> 8;
 }
 
 __device__ __forceinline__ v4i expand_digits(uint32_t x) {
@@ -936,6 +952,276 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Fused screen and score for grouped batches (progressive.py:2428-2606 and
+// :1111-1353). Wave = (16-pair tile z, channel tile ct): the gate row tile ct
+// and the up row tile I/16 + ct, over every rotation block. The blocks run in
+// split order; split s's partial is the fma chain over its blocks and the
+// estimate is ((part_0 + part_1) + part_2) + ... -- the arithmetic of
+// group_screen_kernel followed by score_kernel, with the partials kept in
+// registers. The workgroup's waves share the tile's digit planes in LDS,
+// staged kStageAhead splits ahead (ring of kStageAhead + 1 buffers, one
+// barrier per split); a wave's block steps are loaded one split ahead, each
+// step's successor issued as soon as the step is used. The score epilogue
+// writes the projections and scores of the wave's 16 channels for the tile's
+// pairs. Workgroups past the tiles (one per token) write the zero projections
+// and scores of padded tokens and absent slots.
+
+constexpr int kFusedWaves = 4;
+constexpr int kFusedThreads = 64 * kFusedWaves;
+constexpr int kStageAhead = 1;
+constexpr int kStageBuffers = kStageAhead + 1;
+
+struct FusedScreenArgs {
+  const uint2 *planes;
+  const uint16_t *stats;
+  const int8_t *digits;
+  const int32_t *qexp;
+  const int32_t *qsums;
+  const float *norm2;
+  const int32_t *ids;
+  const float *weights;
+  const uint8_t *padding;
+  const float *norms;
+  const float *geometry;
+  const int32_t *group_experts;
+  const int32_t *group_counts;
+  const int32_t *group_pairs;
+  const int32_t *group_total;
+  float *partial;
+  float *variances;
+  float *scores;
+  uint32_t *tile_masks;  // cleared for the wave's channels (or NULL)
+  int H, I, K, N, T, splits, span, channel_groups, tile_items;
+  int gelu, point;
+};
+
+struct FusedShared {
+  alignas(16) int8_t digits[kStageBuffers][kMaxSpan][3][kPairTile][kDigitStride];
+  int qsum[16][kPairTile];  // blocks (H <= 2048) x pairs
+  int shift[16][kPairTile];
+  float norm2[16][kPairTile];
+  int pair_token[kPairTile], pair_slot[kPairTile];
+};
+
+// One (block, row tile) step's loads: operand words, FP16 scale (and
+// residual) words of the lane's four rows.
+struct StepLoads {
+  uint2 words, scale, residual;
+};
+
+template <bool kGh5>
+__global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreenArgs a) {
+  __shared__ FusedShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int B = a.H / 128;
+  if (static_cast<int>(blockIdx.x) >= a.tile_items) {
+    // zero results of a padded token's slots or of slots with no local expert
+    const int t = blockIdx.x - a.tile_items;
+    if (t >= a.T) return;
+    const bool active = is_active(a.padding, t);
+    for (int k = 0; k < a.K; ++k) {
+      if (active && a.ids[t * a.K + k] >= 0) continue;
+      for (int c = tid; c < a.I; c += kFusedThreads) {
+        const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + c;
+        const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + c;
+        a.partial[base] = 0.0f;
+        a.partial[base + a.N] = 0.0f;
+        if (kGh5) {
+          a.variances[base] = 0.0f;
+          a.variances[base + a.N] = 0.0f;
+        }
+        a.scores[flat] = cfm_score(0.0f, 0.0f, 0.0f, 0.0f, 0.0f, a.weights[t * a.K + k], 0.0f,
+                                   0.0f, a.gelu != 0, a.point != 0);
+      }
+    }
+    return;
+  }
+  const int z = blockIdx.x / a.channel_groups;
+  if (z >= load_uniform(a.group_total)) return;
+  const int CT = a.I / kRowTile, RT = 2 * CT;
+  const int ct = (blockIdx.x % a.channel_groups) * kFusedWaves + wave;
+  const bool working = ct < CT;  // a wave past the channels still stages and waits
+  const int cc = min(ct, CT - 1);
+  const int e = load_uniform(a.group_experts + z);
+  const int count = load_uniform(a.group_counts + z);
+  const int pp = lane % 16, k0 = 16 * (lane / 16), row_in_tile = 4 * (lane / 16);
+  const int span = a.span, splits = a.splits;
+  // the wave's planes and scales: gate row tile cc, up row tile CT + cc
+  const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64 + lane;
+  const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I + row_in_tile;
+  auto load_step = [&](int s, int bl, int up) {
+    StepLoads l;
+    const int b = min(s * span + min(bl, span - 1), B - 1);  // past H: a repeat, unused
+    const int rt = up ? CT + cc : cc;
+    l.words = load_global(planes + (static_cast<long>(b) * RT + rt) * 64);
+    const uint16_t *plane = stats + static_cast<long>(b) * 4 * a.I + kRowTile * rt;
+    l.scale = load_global(reinterpret_cast<const uint2 *>(plane));
+    if (kGh5) l.residual = load_global(reinterpret_cast<const uint2 *>(plane + 2 * a.I));
+    return l;
+  };
+  // split 0's steps in flight while the tile is staged
+  StepLoads step[kMaxSpan][2];
+#pragma unroll
+  for (int bl = 0; bl < kMaxSpan; ++bl)
+#pragma unroll
+    for (int up = 0; up < 2; ++up) step[bl][up] = load_step(0, bl, up);
+
+  // ---- the tile's pairs and per-(block, pair) constants
+  if (tid < kPairTile) {
+    const int pair = tid < count ? a.group_pairs[kGroupPairs * z + tid] : 0;
+    sh.pair_token[tid] = pair / a.K;
+    sh.pair_slot[tid] = pair % a.K;
+  }
+  __syncthreads();
+  for (int i = tid; i < B * kPairTile; i += kFusedThreads) {
+    const int b = i / kPairTile, p = i % kPairTile;
+    const bool live = p < count;
+    const long cell = live ? static_cast<long>(sh.pair_token[p]) * B + b : 0;
+    sh.qsum[b][p] = live ? a.qsums[cell] : 0;
+    sh.shift[b][p] = live ? a.qexp[cell] : 0;
+    sh.norm2[b][p] = live && kGh5 ? a.norm2[cell] : 0.0f;
+  }
+  // staging of split s: rows (block, digit, pair) of 128 bytes, 16 bytes per
+  // thread and item; pairs past the count and blocks past H are zero
+  constexpr int kStageRows = kMaxSpan * 3 * kPairTile;
+  constexpr int kStageItems = kStageRows * 8;  // uint4 per split
+  constexpr int kStagePerThread = (kStageItems + kFusedThreads - 1) / kFusedThreads;
+  auto stage_load = [&](int s, uint4 *held) {
+#pragma unroll
+    for (int j = 0; j < kStagePerThread; ++j) {
+      const int item = tid + j * kFusedThreads;
+      const int row = item / 8, piece = item % 8;
+      const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
+      const int b = s * span + bl;
+      const bool live = s < splits && item < kStageItems && p < count && bl < span && b < B;
+      const long cell = static_cast<long>(sh.pair_token[live ? p : 0]) * B + (live ? b : 0);
+      held[j] = live ? load_global(reinterpret_cast<const uint4 *>(a.digits + (cell * 3 + d) * 128) + piece)
+                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto stage_store = [&](int buffer, const uint4 *held) {
+#pragma unroll
+    for (int j = 0; j < kStagePerThread; ++j) {
+      const int item = tid + j * kFusedThreads;
+      if (item >= kStageItems) break;
+      const int row = item / 8, piece = item % 8;
+      const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
+      *reinterpret_cast<uint4 *>(&sh.digits[buffer][bl][d][p][16 * piece]) = held[j];
+    }
+  };
+  uint4 held[kStagePerThread];
+#pragma unroll
+  for (int q = 0; q < kStageAhead; ++q) {
+    stage_load(q, held);
+    stage_store(q, held);
+  }
+  __syncthreads();
+
+  float est[2][4] = {}, var[2][4] = {};
+  for (int s = 0; s < splits; ++s) {
+    const int buffer = s % kStageBuffers;
+    // split s + kStageAhead's digits go to the buffer split s - 1 used, which
+    // every wave finished before the last barrier
+    stage_load(s + kStageAhead, held);
+    float part[2][4] = {}, vpart[2][4] = {};
+#pragma unroll
+    for (int bl = 0; bl < kMaxSpan; ++bl) {
+      const int b = s * span + bl;
+      const bool live_block = bl < span && b < B;
+      const int qsum = sh.qsum[min(b, B - 1)][pp], shift = sh.shift[min(b, B - 1)][pp];
+      const float n2 = sh.norm2[min(b, B - 1)][pp];
+      const v4i start = v4i{-qsum, -qsum, -qsum, -qsum};
+      auto operand = [&](int h, int d) {
+        return *reinterpret_cast<const v4i *>(&sh.digits[buffer][bl][d][pp][64 * h + k0]);
+      };
+      // gate and up row tiles share each B operand read
+      StepLoads l[2];
+      v4i a0[2], a1[2];
+#pragma unroll
+      for (int up = 0; up < 2; ++up) {
+        l[up] = step[bl][up];
+        step[bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);  // its successor
+        a0[up] = expand_digits(l[up].words.x);
+        a1[up] = expand_digits(l[up].words.y);
+      }
+      if (!live_block) continue;
+      v4i acc[2][3];
+#pragma unroll
+      for (int d = 0; d < 3; ++d) {
+        const v4i b0 = operand(0, d);
+#pragma unroll
+        for (int up = 0; up < 2; ++up)
+          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[up], b0, d == 0 ? start : v4i{0, 0, 0, 0},
+                                                            0, 0, 0);
+      }
+#pragma unroll
+      for (int d = 0; d < 3; ++d) {
+        const v4i b1 = operand(1, d);
+#pragma unroll
+        for (int up = 0; up < 2; ++up)
+          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[up], b1, acc[up][d], 0, 0, 0);
+      }
+#pragma unroll
+      for (int up = 0; up < 2; ++up)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int sum = acc[up][0][r] + (acc[up][1][r] << 8) + (acc[up][2][r] << 16);
+          const float dot = ldexpf(static_cast<float>(sum), -shift);
+          const uint32_t sw = r < 2 ? l[up].scale.x : l[up].scale.y;
+          part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);
+          if (kGh5) {
+            const uint32_t rw = r < 2 ? l[up].residual.x : l[up].residual.y;
+            vpart[up][r] = fmaf(half_at(rw, r & 1), n2, vpart[up][r]);
+          }
+        }
+    }
+#pragma unroll
+    for (int up = 0; up < 2; ++up)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        est[up][r] = s == 0 ? part[up][r] : est[up][r] + part[up][r];
+        if (kGh5) var[up][r] = s == 0 ? vpart[up][r] : var[up][r] + vpart[up][r];
+      }
+    if (s + 1 < splits) {
+      stage_store((s + kStageAhead) % kStageBuffers, held);
+      __syncthreads();
+    }
+  }
+  // ---- score epilogue: lane (pair pp, channels c .. c + 3)
+  if (!working) return;
+  if (a.tile_masks && lane < kRowTile)
+    a.tile_masks[static_cast<long>(z) * a.I + kRowTile * ct + lane] = 0u;
+  if (pp >= count) return;
+  const int token = sh.pair_token[pp], slot = sh.pair_slot[pp];
+  const int c = kRowTile * ct + row_in_tile;
+  const long base = static_cast<long>(token) * 2 * a.N + static_cast<long>(slot) * a.I + c;
+  *reinterpret_cast<float4 *>(a.partial + base) = make_float4(est[0][0], est[0][1], est[0][2], est[0][3]);
+  *reinterpret_cast<float4 *>(a.partial + base + a.N) =
+      make_float4(est[1][0], est[1][1], est[1][2], est[1][3]);
+  if (kGh5) {
+    *reinterpret_cast<float4 *>(a.variances + base) = make_float4(var[0][0], var[0][1], var[0][2], var[0][3]);
+    *reinterpret_cast<float4 *>(a.variances + base + a.N) =
+        make_float4(var[1][0], var[1][1], var[1][2], var[1][3]);
+  }
+  const float weight = a.weights[token * a.K + slot];
+  const float4 norm = *reinterpret_cast<const float4 *>(a.norms + static_cast<long>(e) * a.I + c);
+  const float norms4[4] = {norm.x, norm.y, norm.z, norm.w};
+  float score[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float alpha = 0.0f, beta = 0.0f;
+    if (a.geometry) {
+      alpha = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2];
+      beta = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2 + 1];
+    }
+    score[r] = cfm_score(est[0][r], est[1][r], var[0][r], var[1][r], norms4[r], weight, alpha,
+                         beta, a.gelu != 0, a.point != 0);
+  }
+  *reinterpret_cast<float4 *>(a.scores + static_cast<long>(token) * a.N + static_cast<long>(slot) * a.I + c) =
+      make_float4(score[0], score[1], score[2], score[3]);
+}
+
+// ---------------------------------------------------------------------------
 // score (progressive.py:1111-1353): split sums in split order, then the score
 
 struct ScoreArgs {
@@ -1003,7 +1289,6 @@ __global__ __launch_bounds__(256) void score_kernel(ScoreArgs a) {
   const long flat = static_cast<long>(t) * a.N + logical;
   a.scores[flat] = cfm_score(g, u, vg, vu, norm, a.weights[t * a.K + k], alpha, beta,
                              a.gelu != 0, a.point != 0);
-  a.completed[flat] = 0;
   a.selected[flat] = 0;
 }
 
@@ -1019,6 +1304,7 @@ struct SelectArgs {
   uint32_t *tile_masks;       // [tile][channel] bit p: tile pair p kept it (or NULL)
   int32_t *next_ids;
   uint8_t *selected;
+  uint8_t *completed;  // cleared here; the exact rows set their channels' flags
   int32_t *counts;
   int32_t *starts;
   int32_t *tile_starts;
@@ -1168,6 +1454,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
       ++tied_before;
     }
     a.selected[static_cast<long>(t) * a.N + i] = keep;
+    a.completed[static_cast<long>(t) * a.N + i] = 0;
     const int position = above_before + min(tied_before - (keep && key[j] == cutoff ? 1 : 0), room);
     if (keep) {
       if (key[j] > cutoff) ++above_before;
@@ -2118,6 +2405,7 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.qexp = ws->qexp;
   a.qsums = ws->qsums;
   a.norm2 = ws->norm2;
+  a.digits = ws->digits;
   a.group_experts = ws->group_experts;
   a.group_starts = ws->group_starts;
   a.group_counts = ws->group_counts;
@@ -2206,6 +2494,7 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
       cap * s.K * 4,                          // pair_tiles
       cap * n * 4,                            // tile_masks (tiles * I <= cap * N)
       down_order_words(cap, s) * 4,           // down_order (list + builders' slot records)
+      cap * s.B * 3 * 128,                    // digits
   };
   const int written = count < kWorkspaceBuffers ? count : kWorkspaceBuffers;
   for (int i = 0; i < written; ++i) sizes[i] = table[i];
@@ -2276,6 +2565,13 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     return fail(CFMOE_EINVAL, "trit_planes must be an 8-byte aligned cfmoe_pack_trit_planes output");
   if (s.screened && (!weights->statistics || reinterpret_cast<uintptr_t>(weights->statistics) % 8))
     return fail(CFMOE_EINVAL, "statistics must be 8-byte aligned (the screen loads four at a time)");
+  // the fused screen stores four projections or scores at a time, reads four norms
+  if (s.screened && ((reinterpret_cast<uintptr_t>(workspace->partial) |
+                      reinterpret_cast<uintptr_t>(workspace->variances) |
+                      reinterpret_cast<uintptr_t>(workspace->scores) |
+                      reinterpret_cast<uintptr_t>(workspace->digits) |
+                      reinterpret_cast<uintptr_t>(weights->norms)) % 16))
+    return fail(CFMOE_EINVAL, "partial, variances, scores, digits and norms must be 16-byte aligned");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
   const uint32_t flags = dims->flags;
   const bool gh5 = !(flags & CFMOE_POINT);
@@ -2294,6 +2590,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   sel.threshold = weights->threshold;
   sel.next_ids = workspace->next_ids;
   sel.selected = workspace->selected;
+  sel.completed = workspace->completed;
   sel.counts = workspace->counts;
   sel.starts = workspace->starts;
   sel.tile_starts = workspace->tile_starts;
@@ -2347,7 +2644,48 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     sc.tiles_per_part = static_cast<int>((row_tiles + parts - 1) / parts);
     sc.parts_per_segment = (row_tiles + sc.tiles_per_part - 1) / sc.tiles_per_part;
     const long items = segments * sc.parts_per_segment;
-    if (stages & (1u << CFMOE_STAGE_SCREEN)) {
+    // grouped batches: the fused screen and score (no split partials, no
+    // score launch); smaller ones split the blocks over more workgroups
+    const bool fused = grouped;
+    if ((stages & (1u << CFMOE_STAGE_SCREEN)) && fused) {
+      FusedScreenArgs fs;
+      fs.planes = sc.planes;
+      fs.stats = sc.stats;
+      fs.digits = workspace->digits;
+      fs.qexp = workspace->qexp;
+      fs.qsums = workspace->qsums;
+      fs.norm2 = workspace->norm2;
+      fs.ids = workspace->ids;
+      fs.weights = workspace->weights;
+      fs.padding = padding;
+      fs.norms = weights->norms;
+      fs.geometry = (flags & CFMOE_GEOMETRY) ? weights->geometry : nullptr;
+      fs.group_experts = workspace->group_experts;
+      fs.group_counts = workspace->group_counts;
+      fs.group_pairs = workspace->group_pairs;
+      fs.group_total = workspace->group_total;
+      fs.partial = workspace->partial;
+      fs.variances = workspace->variances;
+      fs.scores = workspace->scores;
+      fs.tile_masks = sel.tile_masks;
+      fs.H = s.H;
+      fs.I = s.I;
+      fs.K = s.K;
+      fs.N = s.N;
+      fs.T = tokens;
+      fs.splits = s.splits;
+      fs.span = s.span;
+      fs.channel_groups = (s.I / kRowTile + kFusedWaves - 1) / kFusedWaves;
+      fs.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * fs.channel_groups;
+      fs.gelu = gelu;
+      fs.point = !gh5;
+      const unsigned blocks = static_cast<unsigned>(fs.tile_items + tokens);
+      if (gh5)
+        hipLaunchKernelGGL(fused_screen_kernel<true>, dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
+      else
+        hipLaunchKernelGGL(fused_screen_kernel<false>, dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
+      if ((rc = check_launch("screen"))) return rc;
+    } else if (stages & (1u << CFMOE_STAGE_SCREEN)) {
       if (gh5)
         hipLaunchKernelGGL(group_screen_kernel<true>, dim3(static_cast<unsigned>(items)),
                            dim3(256), 0, stream, sc);
@@ -2379,7 +2717,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     so.point = !gh5;
     so.tile_masks = sel.tile_masks;
     so.mask_words = tile_bound(tokens, s.K, dims->experts) * s.I;
-    if (stages & (1u << CFMOE_STAGE_SCORE)) {
+    if ((stages & (1u << CFMOE_STAGE_SCORE)) && !fused) {
       hipLaunchKernelGGL(score_kernel, dim3((s.N + 255) / 256, tokens), dim3(256), 0, stream,
                          so);
       if ((rc = check_launch("score"))) return rc;
@@ -2698,7 +3036,7 @@ int cfmoe_forward_noalloc(const cfmoe_dims *dims, const cfmoe_weights *weights,
       reinterpret_cast<void **>(&ws.group_starts), reinterpret_cast<void **>(&ws.group_counts),
       reinterpret_cast<void **>(&ws.group_pairs), reinterpret_cast<void **>(&ws.group_total),
       reinterpret_cast<void **>(&ws.pair_tiles), reinterpret_cast<void **>(&ws.tile_masks),
-      reinterpret_cast<void **>(&ws.down_order),
+      reinterpret_cast<void **>(&ws.down_order), reinterpret_cast<void **>(&ws.digits),
   };
   long offset = 0;
   for (int i = 0; i < kWorkspaceBuffers; ++i) {

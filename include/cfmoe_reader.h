@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 6
+#define CFMOE_ABI_VERSION 7
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -50,13 +50,15 @@ typedef struct ihipStream_t *cfmoe_stream;
 
 /* Stages of one call, in launch order (cfmoe_launch_stage). */
 #define CFMOE_STAGE_PREPARE 0 /* route, rotate, mask, grid quantisation */
-#define CFMOE_STAGE_SCREEN 1  /* sketch projections per block split */
-#define CFMOE_STAGE_SCORE 2   /* split sums and channel scores */
+#define CFMOE_STAGE_SCREEN 1  /* sketch projections per block split; in grouped calls
+                                 also the split sums and channel scores */
+#define CFMOE_STAGE_SCORE 2   /* split sums and channel scores (launches nothing in
+                                 grouped calls) */
 #define CFMOE_STAGE_SELECT 3  /* per-token top-F */
 #define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels (and the encoder, below) */
-#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels; below 16 tokens
-                                 and at rank 32 it runs inside the exact launch, and this
-                                 stage launches nothing */
+#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels; below the grouped
+                                 size and at rank 32 it runs inside the exact launch, and
+                                 this stage launches nothing */
 #define CFMOE_STAGE_DOWN 6    /* down rows of kept channels */
 #define CFMOE_STAGE_OUTPUT 7  /* latent, decoder correction, router mix */
 #define CFMOE_STAGE_COUNT 8
@@ -134,11 +136,13 @@ typedef struct cfmoe_workspace {
   uint32_t *tile_masks;       /* [cap * N] per (tile, channel): bit p set if pair p kept it */
   int32_t *down_order;        /* down workgroups' items grouped by expert per XCD, then the
                                  builders' slot records (size from cfmoe_workspace_sizes) */
+  int8_t *digits;             /* [cap, B, 3, 128] the kept grid values' three balanced
+                                 8-bit digits per rotated coordinate (0 where not kept) */
   double *read_work;          /* [20] read statistics (progressive.py:3507-3515) */
 } cfmoe_workspace;
 
 /* Byte sizes of every workspace buffer, in struct order after `capacity`
- * (32 entries, read_work excluded). Returns the number written. */
+ * (33 entries, read_work excluded). Returns the number written. */
 CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
                           int32_t count);
 
