@@ -39,6 +39,7 @@ from calibration_free_moe.reader.progressive import (  # noqa: E402
     channel_major_down,
 )
 from calibration_free_moe.reader.sketch import block_hadamard_signs, build_sketch  # noqa: E402
+from calibration_free_moe.recovery import subspace_bank  # noqa: E402
 
 METRIC = "sparse MoE-layer decode µs/layer at batch 1/64/128; achieved HBM GB/s on bytes read"
 HBM_PEAK_GBPS = 8000.0
@@ -69,13 +70,8 @@ def device_weights(hidden, width, experts, rank, seed, device, std=0.02):
     gate_up = (torch.randn(experts, 2 * width, hidden, generator=g, device=device) * std).bfloat16()
     down = (torch.randn(experts, hidden, width, generator=g, device=device) * std).bfloat16()
     router = (torch.randn(experts, hidden, generator=g, device=device) * std).bfloat16()
-    gram = torch.einsum("ehi,egi->hg", down.float(), down.float())
-    try:
-        _, vectors = torch.linalg.eigh(gram.double())
-    except RuntimeError:
-        _, vectors = torch.linalg.eigh(gram.double().cpu())
-    u = vectors[:, -rank:].flip(-1).float().to(device)
-    encoder = torch.einsum("hr,ehi->eri", u, down.float()).bfloat16()
+    u, b, _ = subspace_bank(down, rank)
+    encoder = b.bfloat16()
     decoder = u.bfloat16().contiguous()
     codes, stats = build_sketch(gate_up, block_hadamard_signs(hidden, device))
     return {

@@ -732,6 +732,15 @@ __device__ __forceinline__ v4i expand_digits(uint32_t x) {
              static_cast<int>((x >> 4) & 0x03030303u), static_cast<int>((x >> 6) & 0x03030303u)};
 }
 
+// acc0 + 2^8 acc1 + 2^16 acc2 as two shift-adds (v_lshl_add_u32; the empty
+// asm keeps the compiler from re-forming two shifts and a three-way add). The
+// partial sums wrap like the full one, which is below 2^31 in magnitude.
+__device__ __forceinline__ int combine_digits(int acc0, int acc1, int acc2) {
+  uint32_t high = (static_cast<uint32_t>(acc2) << 8) + static_cast<uint32_t>(acc1);
+  asm volatile("" : "+v"(high));
+  return static_cast<int>((high << 8) + static_cast<uint32_t>(acc0));
+}
+
 __device__ __forceinline__ float half_at(uint32_t word, int high) {
   return static_cast<float>(
       __builtin_bit_cast(_Float16, static_cast<uint16_t>(high ? word >> 16 : word & 0xffffu)));
@@ -915,7 +924,7 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
         acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, operand(bl, 1, d), acc[d], 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int sum = acc[0][r] + (acc[1][r] << 8) + (acc[2][r] << 16);
+        const int sum = combine_digits(acc[0][r], acc[1][r], acc[2][r]);
         const float dot = ldexpf(static_cast<float>(sum), -shift[bl]);
         const uint32_t sw = r < 2 ? tile.scale[bl].x : tile.scale[bl].y;
         part[r] = fmaf(dot, half_at(sw, r & 1), part[r]);
@@ -1165,7 +1174,7 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
       for (int up = 0; up < 2; ++up)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int sum = acc[up][0][r] + (acc[up][1][r] << 8) + (acc[up][2][r] << 16);
+          const int sum = combine_digits(acc[up][0][r], acc[up][1][r], acc[up][2][r]);
           const float dot = ldexpf(static_cast<float>(sum), -shift);
           const uint32_t sw = r < 2 ? l[up].scale.x : l[up].scale.y;
           part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);

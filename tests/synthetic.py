@@ -17,6 +17,7 @@ import torch
 from torch import Tensor
 
 from calibration_free_moe.reader.progressive import recovery_geometry
+from calibration_free_moe.recovery import subspace_bank
 from calibration_free_moe.reader.sketch import block_hadamard_signs, build_sketch
 
 
@@ -67,18 +68,9 @@ def zipf_route(tokens: int, experts: int, top_k: int, generator: torch.Generator
 
 
 def recovery_bank(down: Tensor, rank: int) -> tuple[Tensor, Tensor]:
-    """U [H, R] and B [E, R, I] from the down weights [E, H, I] (BF16 outputs)."""
-    d = down.double() if down.device.type == "cpu" else down.float()
-    gram = torch.zeros(d.shape[1], d.shape[1], dtype=d.dtype, device=d.device)
-    for expert in range(d.shape[0]):
-        gram += d[expert] @ d[expert].T
-    try:
-        _, vectors = torch.linalg.eigh(gram)
-    except RuntimeError:  # no device eigensolver: solve on the host
-        _, vectors = torch.linalg.eigh(gram.double().cpu())
-        vectors = vectors.to(d.device, d.dtype)
-    u = vectors[:, -rank:].flip(-1)
-    b = torch.einsum("hr,ehi->eri", u, d)
+    """B [E, R, I] and U [H, R] of the down weights [E, H, I], cast to BF16
+    (the package's subspace_bank, on the device of `down`)."""
+    u, b, _ = subspace_bank(down, rank)
     return b.to(torch.bfloat16), u.to(torch.bfloat16)
 
 

@@ -4,6 +4,7 @@
 they are recomputed from the materialised per-channel response U b_c.
 """
 
+import pytest
 import torch
 
 from calibration_free_moe.reader.progressive import recovery_geometry
@@ -31,3 +32,35 @@ def test_geometry_equals_the_materialised_response():
     energy = (encoder_t.double() @ decoder.double().T).square().sum(-1)
     torch.testing.assert_close(got[..., 0].square() + got[..., 1].square(), energy,
                                rtol=1e-5, atol=1e-9)
+
+
+def test_subspace_bank_against_the_singular_vectors():
+    """U spans the top-r left singular vectors of the stacked down columns
+    (an SVD, not the Gram eigensolver), captured is their energy share, and
+    U B_e is the projection of D_e onto that subspace."""
+    from calibration_free_moe.recovery import subspace_bank
+
+    generator = torch.Generator().manual_seed(4)
+    experts, hidden, width, rank = 5, 96, 40, 6
+    # a decaying spectrum so that the top-r subspace is well separated
+    basis = torch.linalg.qr(torch.randn(hidden, hidden, generator=generator, dtype=torch.float64))[0]
+    scales = torch.logspace(0, -2, hidden, dtype=torch.float64)
+    mix = torch.randn(experts, hidden, width, generator=generator, dtype=torch.float64)
+    down = ((basis * scales) @ mix).to(torch.bfloat16)
+    u, b, captured = subspace_bank(down, rank, chunk=2)
+    assert u.shape == (hidden, rank) and b.shape == (experts, rank, width)
+    assert u.dtype == b.dtype == torch.float64
+    columns = down.double().permute(1, 0, 2).reshape(hidden, -1)
+    left, singular, _ = torch.linalg.svd(columns, full_matrices=False)
+    top = left[:, :rank]
+    torch.testing.assert_close(u @ u.T, top @ top.T, rtol=0, atol=1e-9)
+    energy = singular.square()
+    assert abs(captured - float(energy[:rank].sum() / energy.sum())) < 1e-12
+    torch.testing.assert_close(u.T @ u, torch.eye(rank, dtype=torch.float64), rtol=0, atol=1e-12)
+    for e in range(experts):
+        projection = top @ (top.T @ down[e].double())
+        torch.testing.assert_close(u @ b[e], projection, rtol=0, atol=1e-9)
+    # chunking does not change the result
+    u2, b2, captured2 = subspace_bank(down, rank, chunk=16)
+    torch.testing.assert_close(u2 @ b2[1], u @ b[1], rtol=0, atol=1e-12)
+    assert captured2 == pytest.approx(captured, abs=1e-14)
