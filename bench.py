@@ -154,8 +154,8 @@ def algorithmic_bytes(reader: ProgressiveReader, tokens: int) -> dict[str, int]:
 STAGE_BYTES = {"screen": ("sketch",), "exact": ("gate_up",), "down": ("down",),
                "encode": ("encoder",)}
 DIRECT_RANK = 32  # rank at which grouped batches run the encoder inside the exact launch
-STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "group_screen_kernel",
-                 "score": "score_kernel", "select": "select_kernel", "exact": "exact_kernel",
+STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "small_screen_kernel",
+                 "select": "select_kernel", "exact": "exact_kernel",
                  "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
 GROUP_EXACT_TOKENS = GROUPED_TOKENS  # batches from which the exact stage runs group_exact_kernel
 
@@ -177,8 +177,8 @@ def stage_bytes(stage: str, tokens: int, rank: int) -> tuple[str, ...]:
 
 
 def stage_kernel(stage: str, tokens: int) -> str:
-    """Name of the kernel a stage launches at this batch size (grouped
-    batches: the screen launch also scores, the score stage launches nothing)."""
+    """Name of the kernel a stage launches at this batch size (the screen
+    launch also scores; the score stage launches nothing)."""
     if stage == "exact" and tokens >= GROUP_EXACT_TOKENS:
         return "group_exact_kernel"
     if stage == "screen" and tokens >= GROUP_EXACT_TOKENS:

@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 POINT = 1
 GELU = 2
@@ -72,8 +72,6 @@ WORKSPACE_FIELDS = (
     ("norm2", "float32"),
     ("partial", "float32"),
     ("variances", "float32"),
-    ("screen_parts", "float32"),
-    ("screen_variance_parts", "float32"),
     ("scores", "float32"),
     ("next_ids", "int32"),
     ("selected", "bool"),

@@ -200,7 +200,6 @@ class ReaderWorkspace:
             return tensor
 
         self.screen_splits = _screen_splits(h) if plan.completion_count < n else 1
-        splits = _screen_splits(h)
         self.ids = buffer("ids", (capacity, k))
         self.weights = buffer("weights", (capacity, k))
         self.sketch_planes = buffer("planes", (capacity, blocks, keep))
@@ -215,10 +214,10 @@ class ReaderWorkspace:
         self.sketch_norms = buffer("norm2", (capacity, blocks))
         self.partial = buffer("partial", (capacity, 2, n))
         self.variances = buffer("variances", (capacity, 2, n))
-        self.screen_parts = buffer("screen_parts", (capacity * splits, 2, n))
-        self.screen_variance_parts = buffer(
-            "screen_variance_parts", (capacity * splits, 2, n)
-        )
+        # the reference's split partials: this build keeps them in registers
+        # and LDS inside the screen launch, so the buffers are empty
+        self.screen_parts = torch.empty((0, 2, n), dtype=torch.float32, device=device)
+        self.screen_variance_parts = torch.empty((0, 2, n), dtype=torch.float32, device=device)
         self.activations = buffer("activations", (capacity, n))
         self.completed = buffer("completed", (capacity, n))
         self.selected = buffer("selected", (capacity, n))
@@ -280,7 +279,7 @@ class ReaderWorkspace:
             self.ids, self.weights, self.sketch_planes, self.sketch_coordinates,
             self.sketch_values, self.sketch_exponents, self.sketch_sums, self.sketch_norms,
             self.partial,
-            self.variances, self.screen_parts, self.screen_variance_parts,
+            self.variances,
             self.activations, self.completed, self.selected, *self.candidate_ids,
             *self.scores, self.starts, self.counts, self.tile_starts,
             self.down_tile_starts, self.down_parts, self.encoder_parts, self.latent,
@@ -313,8 +312,6 @@ _WORKSPACE_ATTRS = (
     ("norm2", "sketch_norms"),
     ("partial", "partial"),
     ("variances", "variances"),
-    ("screen_parts", "screen_parts"),
-    ("screen_variance_parts", "screen_variance_parts"),
     ("selected", "selected"),
     ("completed", "completed"),
     ("activations", "activations"),

@@ -6,8 +6,11 @@
 // (calibration_free_moe/reader/progressive.py:3876-4472):
 //
 //   prepare_kernel   route, expert grouping, rotate + mask + grid (:143-453)
-//   group_screen_kernel  expert-major sketch projections (MFMA)   (:478-1108)
-//   score_kernel     split sums, BF16 rounding, channel scores   (:1111-1353)
+//   small_screen_kernel  sketch projections and scores, batches below the
+//                    grouped size: a tile's channel tile per workgroup, its
+//                    block splits over the waves (MFMA)   (:478-1108, :1111-1353)
+//   fused_screen_kernel  the same for grouped batches: every split of a
+//                    channel tile in one wave             (:2428-2606)
 //   select_kernel    per-token top-F (radix select + compaction) (:1584-1775)
 //   exact_kernel     native gate/up rows of kept channels         (:1372-1581)
 //   encode_kernel    recovery encoder over skipped channels       (:1859-2016)
@@ -323,7 +326,7 @@ struct PrepareArgs {
 };
 
 constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
-constexpr int kWorkspaceBuffers = 33;  // cfmoe_workspace pointers after capacity
+constexpr int kWorkspaceBuffers = 31;  // cfmoe_workspace pointers after capacity
 constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 constexpr int kPrepareThreads = 256;
@@ -746,219 +749,274 @@ __device__ __forceinline__ float half_at(uint32_t word, int high) {
       __builtin_bit_cast(_Float16, static_cast<uint16_t>(high ? word >> 16 : word & 0xffffu)));
 }
 
-// Screen workgroup = (tile z, block split s, range of row tiles). The tile's
-// pairs' kept grid values are staged once as three int8 digit planes
-// ([block][digit][pair][coordinate], zero at coordinates a pair did not keep)
-// and held in registers as MFMA B operands; each wave then walks its row tiles
-// with no barrier: load the row tile's planes and FP16 scales (one tile ahead),
-// expand the digits t + 1, and contract with v_mfma_i32_16x16x64_i8 (16 rows x
-// 16 pairs x 64 coordinates, two halves, one MFMA per grid digit). The digit-0
-// chain starts from -sum(q), so acc0 + acc1 256 + acc2 65536 is the exact
-// integer sum of t q over the kept coordinates; the block's grid exponent and
-// FP16 scale then feed the split's FMA chain in block order
-// (progressive.py:1111-1160).
+// Zero projections and scores of a padded token's slots and of slots with no
+// local expert (the screens cover only grouped pairs); `threads` of the
+// workgroup share the channels.
+template <bool kGh5, class Args>
+__device__ void score_absent_slots(const Args &a, int t, int threads) {
+  const bool active = is_active(a.padding, t);
+  for (int k = 0; k < a.K; ++k) {
+    if (active && a.ids[t * a.K + k] >= 0) continue;
+    for (int c = threadIdx.x; c < a.I; c += threads) {
+      const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + c;
+      const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + c;
+      a.partial[base] = 0.0f;
+      a.partial[base + a.N] = 0.0f;
+      if (kGh5) {
+        a.variances[base] = 0.0f;
+        a.variances[base + a.N] = 0.0f;
+      }
+      a.scores[flat] = cfm_score(0.0f, 0.0f, 0.0f, 0.0f, 0.0f, a.weights[t * a.K + k], 0.0f, 0.0f,
+                                 a.gelu != 0, a.point != 0);
+    }
+  }
+}
 
-struct GroupScreenArgs {
+// Score of four channels for one pair from the gate and up estimates (and
+// variances); writes the projections, variances and scores
+// (progressive.py:1265-1353).
+template <bool kGh5, class Args>
+__device__ __forceinline__ void score_four(const Args &a, int e, int token, int slot, int c,
+                                           const float gate[4], const float up[4],
+                                           const float gate_var[4], const float up_var[4]) {
+  const long base = static_cast<long>(token) * 2 * a.N + static_cast<long>(slot) * a.I + c;
+  *reinterpret_cast<float4 *>(a.partial + base) = make_float4(gate[0], gate[1], gate[2], gate[3]);
+  *reinterpret_cast<float4 *>(a.partial + base + a.N) = make_float4(up[0], up[1], up[2], up[3]);
+  if (kGh5) {
+    *reinterpret_cast<float4 *>(a.variances + base) =
+        make_float4(gate_var[0], gate_var[1], gate_var[2], gate_var[3]);
+    *reinterpret_cast<float4 *>(a.variances + base + a.N) =
+        make_float4(up_var[0], up_var[1], up_var[2], up_var[3]);
+  }
+  const float weight = a.weights[token * a.K + slot];
+  const float4 norm = *reinterpret_cast<const float4 *>(a.norms + static_cast<long>(e) * a.I + c);
+  const float norms4[4] = {norm.x, norm.y, norm.z, norm.w};
+  float score[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float alpha = 0.0f, beta = 0.0f;
+    if (a.geometry) {
+      alpha = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2];
+      beta = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2 + 1];
+    }
+    score[r] = cfm_score(gate[r], up[r], gate_var[r], up_var[r], norms4[r], weight, alpha, beta,
+                         a.gelu != 0, a.point != 0);
+  }
+  *reinterpret_cast<float4 *>(a.scores + static_cast<long>(token) * a.N + static_cast<long>(slot) * a.I + c) =
+      make_float4(score[0], score[1], score[2], score[3]);
+}
+
+// ---------------------------------------------------------------------------
+// Screen and score below the grouped size (progressive.py:478-1108,
+// :1111-1353). Workgroup = (16-pair tile z, channel tile ct: gate row tile
+// ct and up row tile I/16 + ct); wave w takes the block splits
+// [w S / 4, (w + 1) S / 4) and stages, for the tile's live pairs only, those
+// blocks' digit planes in its own LDS area (no barrier: a wave reads only what
+// it wrote, and its LDS operations complete in order). Per split the wave
+// forms the partial (fma chain over the split's blocks) of its 2 x 4 rows for
+// every pair, and leaves it in LDS; after one barrier wave 0 sums the splits
+// in order, ((part_0 + part_1) + part_2) + ..., and scores the 16 channels.
+// The MFMA contraction is that of the fused screen (B operands of pairs past
+// the count are zero registers, not LDS reads). Workgroups from tile_items
+// on (one per token) write the zero results of padded tokens and absent slots.
+
+constexpr int kSmallWaves = 4;
+constexpr int kMaxSplits = 8;
+
+struct SmallScreenArgs {
   const uint2 *planes;
   const uint16_t *stats;
-  const int32_t *coords;
-  const int32_t *qvals;
+  const int8_t *digits;
   const int32_t *qexp;
   const int32_t *qsums;
   const float *norm2;
   const int32_t *group_experts;
-  const int32_t *group_starts;
   const int32_t *group_counts;
   const int32_t *group_pairs;
   const int32_t *group_total;
-  float *parts;
-  float *vparts;
-  int H, I, K, N, keep, splits, span, parts_per_segment, tiles_per_part;
+  const int32_t *ids;
+  const float *weights;
+  const uint8_t *padding;
+  const float *norms;
+  const float *geometry;
+  float *partial;
+  float *variances;
+  float *scores;
+  int H, I, K, N, T, splits, span, tile_items, max_pairs;
+  int gelu, point;
 };
 
-struct ScreenShared {
-  alignas(16) int8_t digits[kMaxSpan][3][kPairTile][kDigitStride];
-  int pair_token[kPairTile], pair_slot[kPairTile];
-  int qsum[kMaxSpan][kPairTile];
-  int shift[kMaxSpan][kPairTile];
-  float norm2[kMaxSpan][kPairTile];
-};
-
-// One row tile's loads: both blocks' operand words and FP16 scale (and
+// One (block, row tile) step's loads: operand words, FP16 scale (and
 // residual) words of the lane's four rows.
-struct RowTileLoads {
-  uint2 words[kMaxSpan];
-  uint2 scale[kMaxSpan];
-  uint2 residual[kMaxSpan];
+struct StepLoads {
+  uint2 words, scale, residual;
 };
+
+constexpr int kWaveSplits = (kMaxSplits + kSmallWaves - 1) / kSmallWaves;
+constexpr int kWaveBlocks = kWaveSplits * kMaxSpan;
+
+// Dynamic LDS bytes of small_screen_kernel for tiles of at most `max_pairs`.
+__host__ __device__ inline long small_screen_lds(int max_pairs) {
+  return static_cast<long>(kSmallWaves) * kWaveBlocks * 3 * max_pairs * kDigitStride;
+}
 
 template <bool kGh5>
-__global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
-  __shared__ ScreenShared sh;
+__global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScreenArgs a) {
+  // per wave: its blocks' digit rows [block][digit][pair < max_pairs][kDigitStride]
+  extern __shared__ __align__(16) int8_t small_digits[];
+  __shared__ float parts[kMaxSplits][2][64][4];
+  __shared__ float vparts[kGh5 ? kMaxSplits : 1][2][64][4];
+  __shared__ int pair_token[kPairTile], pair_slot[kPairTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int segment = blockIdx.x / a.parts_per_segment;
-  const int part = blockIdx.x % a.parts_per_segment;
-  const int z = segment / a.splits, s = segment % a.splits;
-  if (z >= *a.group_total) return;
+  if (static_cast<int>(blockIdx.x) >= a.tile_items) {
+    const int t = blockIdx.x - a.tile_items;
+    if (t < a.T) score_absent_slots<kGh5>(a, t, 64 * kSmallWaves);
+    return;
+  }
+  const int CT = a.I / kRowTile, RT = 2 * CT;
+  const int z = blockIdx.x / CT, ct = blockIdx.x % CT;
+  if (z >= load_uniform(a.group_total)) return;
   const int B = a.H / 128;
-  const int RT = 2 * a.I / kRowTile;
-  const int rt_begin = part * a.tiles_per_part;
-  const int rt_end = min(RT, rt_begin + a.tiles_per_part);
-  if (rt_begin >= rt_end) return;
-  const int e = a.group_experts[z];
-  const int first_pair = a.group_starts[z];
-  const int count = a.group_counts[z];
-  const int b_begin = s * a.span, blocks = min(B, b_begin + a.span) - b_begin;
-  const int keep = a.keep;
-
-  // the trit planes and scales depend only on the expert and the split: the
-  // wave's first row tile is loaded while the tile's digits are staged
-  const int row_in_tile = 4 * (lane / 16);
-  const uint2 *planes = a.planes + (static_cast<long>(e) * B + b_begin) * RT * 64 + lane;
-  const uint16_t *stats = a.stats + (static_cast<long>(e) * B + b_begin) * 4 * a.I + row_in_tile;
-  const int second = blocks > 1 ? 1 : 0;  // block offset of the second load (repeats a lone block)
-  auto load = [=](int rt) {
-    RowTileLoads t;
+  const int e = load_uniform(a.group_experts + z);
+  const int count = load_uniform(a.group_counts + z);
+  const int pp = lane % 16, k0 = 16 * (lane / 16), row_in_tile = 4 * (lane / 16);
+  const int span = a.span, splits = a.splits;
+  const int per_wave = (splits + kSmallWaves - 1) / kSmallWaves;
+  const int s_begin = wave * per_wave, s_end = min(splits, s_begin + per_wave);
+  const int b_begin = s_begin * span;
+  // the wave's steps (split si, block j, gate/up) are loaded first
+  const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64 + lane;
+  const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I + row_in_tile;
+  StepLoads step[kWaveSplits][kMaxSpan][2];
 #pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl) {
-      const int block = bl ? second : 0;
-      t.words[bl] = load_global(planes + (block * RT + rt) * 64);
-      t.scale[bl] = load_global(reinterpret_cast<const uint2 *>(
-          stats + block * 4 * a.I + kRowTile * rt));
-      if (kGh5)
-        t.residual[bl] = load_global(reinterpret_cast<const uint2 *>(
-            stats + block * 4 * a.I + 2 * a.I + kRowTile * rt));
-    }
-    return t;
-  };
-  int rt = rt_begin + wave;
-  RowTileLoads current = load(min(rt, rt_end - 1));
-
-  // ---- stage the tile's digits, grid exponents and sums
-  for (int i = tid; i < static_cast<int>(sizeof(sh.digits) / 16); i += 256)
-    reinterpret_cast<uint4 *>(&sh.digits[0][0][0][0])[i] = make_uint4(0u, 0u, 0u, 0u);
-  if (tid < count) {
-    const int pair = a.group_pairs[first_pair + tid];
-    sh.pair_token[tid] = pair / a.K;
-    sh.pair_slot[tid] = pair % a.K;
+  for (int si = 0; si < kWaveSplits; ++si)
+#pragma unroll
+    for (int j = 0; j < kMaxSpan; ++j)
+#pragma unroll
+      for (int up = 0; up < 2; ++up) {
+        const int b = min((s_begin + si) * span + j, B - 1);  // past the range: unused
+        const int rt = up ? CT + ct : ct;
+        step[si][j][up].words = load_global(planes + (static_cast<long>(b) * RT + rt) * 64);
+        const uint16_t *plane = stats + static_cast<long>(b) * 4 * a.I + kRowTile * rt;
+        step[si][j][up].scale = load_global(reinterpret_cast<const uint2 *>(plane));
+        if (kGh5)
+          step[si][j][up].residual = load_global(reinterpret_cast<const uint2 *>(plane + 2 * a.I));
+      }
+  if (tid < kPairTile) {
+    const int pair = tid < count ? a.group_pairs[kGroupPairs * z + tid] : 0;
+    pair_token[tid] = pair / a.K;
+    pair_slot[tid] = pair % a.K;
   }
   __syncthreads();
-  if (tid < kMaxSpan * kPairTile) {
-    const int bl = tid / kPairTile, pp = tid % kPairTile;
-    const bool live = bl < blocks && pp < count;
-    const long cell = live ? static_cast<long>(sh.pair_token[pp]) * B + b_begin + bl : 0;
-    sh.qsum[bl][pp] = live ? a.qsums[cell] : 0;
-    sh.shift[bl][pp] = live ? a.qexp[cell] : 0;
-    sh.norm2[bl][pp] = live && kGh5 ? a.norm2[cell] : 0.0f;
+  const bool live_pair = pp < count;
+  const long pair_cell = static_cast<long>(pair_token[min(pp, count - 1)]) * B;
+  // the lane's pair's grid sums, exponents (and kept norms) of the wave's blocks
+  int qsum[kWaveSplits][kMaxSpan], shift[kWaveSplits][kMaxSpan];
+  float n2[kWaveSplits][kMaxSpan];
+#pragma unroll
+  for (int si = 0; si < kWaveSplits; ++si)
+#pragma unroll
+    for (int j = 0; j < kMaxSpan; ++j) {
+      const long cell = pair_cell + min((s_begin + si) * span + j, B - 1);
+      qsum[si][j] = live_pair ? load_global(a.qsums + cell) : 0;
+      shift[si][j] = live_pair ? load_global(a.qexp + cell) : 0;
+      n2[si][j] = kGh5 && live_pair ? load_global(a.norm2 + cell) : 0.0f;
+    }
+  // stage the wave's blocks for the live pairs: rows (block, digit, pair) of
+  // 128 bytes, eight lanes per row
+  int8_t *mine = small_digits + static_cast<long>(wave) * kWaveBlocks * 3 * a.max_pairs * kDigitStride;
+  const int wave_rows = max(0, min(B, s_end * span) - min(B, b_begin)) * 3 * count;
+  for (int item = lane; item < wave_rows * 8; item += 64) {
+    const int row = item / 8, piece = item % 8;
+    const int bl = row / (3 * count), d = (row / count) % 3, p = row % count;
+    const long cell = static_cast<long>(pair_token[p]) * B + b_begin + bl;
+    const uint4 v = load_global(reinterpret_cast<const uint4 *>(a.digits + (cell * 3 + d) * 128) + piece);
+    *reinterpret_cast<uint4 *>(mine + ((bl * 3 + d) * a.max_pairs + p) * kDigitStride + 16 * piece) = v;
   }
-  {
-    // thread (block bl, kept position j) over the tile's pairs; all loads of
-    // a group of four pairs are issued before any is used
-    const int bl = tid >> 7, j = tid & 127;
-    const bool lane_live = bl < blocks && j < keep;
-    const int jj = min(j, keep - 1);
-    const int block = b_begin + min(bl, blocks - 1);
+  const int my_row = min(pp, count - 1);
 #pragma unroll
-    for (int group = 0; group < kPairTile / 4; ++group) {
-      if (4 * group >= count) break;
-      int coord[4], q[4];
+  for (int si = 0; si < kWaveSplits; ++si) {
+    const int s = s_begin + si;
+    if (s >= s_end) break;
+    float part[2][4] = {}, vpart[2][4] = {};
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pp = min(4 * group + r, count - 1);
-        const long base = (static_cast<long>(sh.pair_token[pp]) * B + block) * keep + jj;
-        coord[r] = keep < 128 ? a.coords[base] : jj;
-        q[r] = a.qvals[base];
+    for (int j = 0; j < kMaxSpan; ++j) {
+      const int b = s * span + j;
+      if (j >= span || b >= B) break;
+      const int bl = b - b_begin;
+      const v4i start = v4i{-qsum[si][j], -qsum[si][j], -qsum[si][j], -qsum[si][j]};
+      auto operand = [&](int h, int d) {
+        const v4i v = *reinterpret_cast<const v4i *>(
+            mine + ((bl * 3 + d) * a.max_pairs + my_row) * kDigitStride + 64 * h + k0);
+        return live_pair ? v : v4i{0, 0, 0, 0};
+      };
+      v4i a0[2], a1[2];
+#pragma unroll
+      for (int up = 0; up < 2; ++up) {
+        a0[up] = expand_digits(step[si][j][up].words.x);
+        a1[up] = expand_digits(step[si][j][up].words.y);
+      }
+      v4i acc[2][3];
+#pragma unroll
+      for (int d = 0; d < 3; ++d) {
+        const v4i b0 = operand(0, d);
+#pragma unroll
+        for (int up = 0; up < 2; ++up)
+          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[up], b0, d == 0 ? start : v4i{0, 0, 0, 0},
+                                                            0, 0, 0);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pp = 4 * group + r;
-        if (lane_live && pp < count) {
-          int d0, d1, d2;
-          grid_digits(q[r], d0, d1, d2);
-          sh.digits[bl][0][pp][coord[r]] = static_cast<int8_t>(d0);
-          sh.digits[bl][1][pp][coord[r]] = static_cast<int8_t>(d1);
-          sh.digits[bl][2][pp][coord[r]] = static_cast<int8_t>(d2);
+      for (int d = 0; d < 3; ++d) {
+        const v4i b1 = operand(1, d);
+#pragma unroll
+        for (int up = 0; up < 2; ++up)
+          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[up], b1, acc[up][d], 0, 0, 0);
+      }
+#pragma unroll
+      for (int up = 0; up < 2; ++up)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int sum = combine_digits(acc[up][0][r], acc[up][1][r], acc[up][2][r]);
+          const float dot = ldexpf(static_cast<float>(sum), -shift[si][j]);
+          const uint32_t sw = r < 2 ? step[si][j][up].scale.x : step[si][j][up].scale.y;
+          part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);
+          if (kGh5) {
+            const uint32_t rw = r < 2 ? step[si][j][up].residual.x : step[si][j][up].residual.y;
+            vpart[up][r] = fmaf(half_at(rw, r & 1), n2[si][j], vpart[up][r]);
+          }
         }
-      }
+    }
+#pragma unroll
+    for (int up = 0; up < 2; ++up) {
+      *reinterpret_cast<float4 *>(&parts[s][up][lane][0]) =
+          make_float4(part[up][0], part[up][1], part[up][2], part[up][3]);
+      if (kGh5)
+        *reinterpret_cast<float4 *>(&vparts[s][up][lane][0]) =
+            make_float4(vpart[up][0], vpart[up][1], vpart[up][2], vpart[up][3]);
     }
   }
   __syncthreads();
-
-  // ---- B operands and per-pair constants of this lane's pair column
-  const int pp = lane % 16, k0 = 16 * (lane / 16);
-  // B operands are read from LDS per row tile (holding all twelve would
-  // cost 48 registers and half the waves per SIMD)
-  auto operand = [&](int bl, int h, int d) {
-    return *reinterpret_cast<const v4i *>(&sh.digits[bl][d][pp][64 * h + k0]);
-  };
-  v4i start[kMaxSpan];
-  int shift[kMaxSpan];
-  float norm2[kMaxSpan];
+  if (wave != 0 || !live_pair) return;
+  float est[2][4], var[2][4] = {};
 #pragma unroll
-  for (int bl = 0; bl < kMaxSpan; ++bl) {
-    const int qsum = sh.qsum[bl][pp];
-    start[bl] = v4i{-qsum, -qsum, -qsum, -qsum};
-    shift[bl] = sh.shift[bl][pp];
-    norm2[bl] = sh.norm2[bl][pp];
-  }
-  const bool store_lane = pp < count;
-  const int token = sh.pair_token[min(pp, count - 1)], slot = sh.pair_slot[min(pp, count - 1)];
-  // element offsets below 2^31: capacity * K <= 8192, splits <= 8, N <= 16384
-  const uint32_t lane_base = static_cast<uint32_t>((token * a.splits + s) * 2 * a.N + slot * a.I);
-  if (rt >= rt_end) return;
-  auto process = [&](const RowTileLoads &tile, int rt_now) {
-    float part[4] = {0.0f, 0.0f, 0.0f, 0.0f}, vpart[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int up = 0; up < 2; ++up)
 #pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl) {
-      if (bl >= blocks) break;
-      const v4i a0 = expand_digits(tile.words[bl].x);
-      const v4i a1 = expand_digits(tile.words[bl].y);
-      v4i acc[3];
-      acc[0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand(bl, 0, 0), start[bl], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand(bl, 0, 1), v4i{0, 0, 0, 0}, 0,
-                                                     0, 0);
-      acc[2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, operand(bl, 0, 2), v4i{0, 0, 0, 0}, 0,
-                                                     0, 0);
+    for (int r = 0; r < 4; ++r) {
+      est[up][r] = parts[0][up][lane][r];
+      if (kGh5) var[up][r] = vparts[0][up][lane][r];
+    }
+  for (int s = 1; s < splits; ++s)
 #pragma unroll
-      for (int d = 0; d < 3; ++d)
-        acc[d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, operand(bl, 1, d), acc[d], 0, 0, 0);
+    for (int up = 0; up < 2; ++up)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int sum = combine_digits(acc[0][r], acc[1][r], acc[2][r]);
-        const float dot = ldexpf(static_cast<float>(sum), -shift[bl]);
-        const uint32_t sw = r < 2 ? tile.scale[bl].x : tile.scale[bl].y;
-        part[r] = fmaf(dot, half_at(sw, r & 1), part[r]);
-        if (kGh5) {
-          const uint32_t rw = r < 2 ? tile.residual[bl].x : tile.residual[bl].y;
-          vpart[r] = fmaf(half_at(rw, r & 1), norm2[bl], vpart[r]);
-        }
+        est[up][r] = est[up][r] + parts[s][up][lane][r];
+        if (kGh5) var[up][r] = var[up][r] + vparts[s][up][lane][r];
       }
-    }
-    if (store_lane) {
-      const int row = kRowTile * rt_now + row_in_tile;
-      const int gate_up = row >= a.I ? 1 : 0, channel = row - gate_up * a.I;
-      const uint32_t offset = lane_base + static_cast<uint32_t>(gate_up * a.N + channel);
-      *reinterpret_cast<float4 *>(a.parts + offset) = make_float4(part[0], part[1], part[2], part[3]);
-      if (kGh5)
-        *reinterpret_cast<float4 *>(a.vparts + offset) =
-            make_float4(vpart[0], vpart[1], vpart[2], vpart[3]);
-    }
-  };
-  // three of the wave's row tiles in flight (a load past the range repeats
-  // its last row tile)
-  RowTileLoads second_tile = load(min(rt + 4, rt_end - 1));
-  RowTileLoads third_tile = load(min(rt + 8, rt_end - 1));
-  for (; rt < rt_end; rt += 12) {
-    process(current, rt);
-    current = load(min(rt + 12, rt_end - 1));
-    if (rt + 4 >= rt_end) break;
-    process(second_tile, rt + 4);
-    second_tile = load(min(rt + 16, rt_end - 1));
-    if (rt + 8 >= rt_end) break;
-    process(third_tile, rt + 8);
-    third_tile = load(min(rt + 20, rt_end - 1));
-  }
+  score_four<kGh5>(a, e, pair_token[pp], pair_slot[pp], kRowTile * ct + row_in_tile, est[0], est[1],
+                   var[0], var[1]);
 }
+
 
 // ---------------------------------------------------------------------------
 // Fused screen and score for grouped batches (progressive.py:2428-2606 and
@@ -966,8 +1024,7 @@ __global__ __launch_bounds__(256) void group_screen_kernel(GroupScreenArgs a) {
 // and the up row tile I/16 + ct, over every rotation block. The blocks run in
 // split order; split s's partial is the fma chain over its blocks and the
 // estimate is ((part_0 + part_1) + part_2) + ... -- the arithmetic of
-// group_screen_kernel followed by score_kernel, with the partials kept in
-// registers. The workgroup's waves share the tile's digit planes in LDS,
+// small_screen_kernel, with the partials kept in registers. The workgroup's waves share the tile's digit planes in LDS,
 // staged kStageAhead splits ahead (ring of kStageAhead + 1 buffers, one
 // barrier per split); a wave's block steps are loaded one split ahead, each
 // step's successor issued as soon as the step is used. The score epilogue
@@ -1012,37 +1069,14 @@ struct FusedShared {
   int pair_token[kPairTile], pair_slot[kPairTile];
 };
 
-// One (block, row tile) step's loads: operand words, FP16 scale (and
-// residual) words of the lane's four rows.
-struct StepLoads {
-  uint2 words, scale, residual;
-};
-
 template <bool kGh5>
 __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreenArgs a) {
   __shared__ FusedShared sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int B = a.H / 128;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
-    // zero results of a padded token's slots or of slots with no local expert
     const int t = blockIdx.x - a.tile_items;
-    if (t >= a.T) return;
-    const bool active = is_active(a.padding, t);
-    for (int k = 0; k < a.K; ++k) {
-      if (active && a.ids[t * a.K + k] >= 0) continue;
-      for (int c = tid; c < a.I; c += kFusedThreads) {
-        const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + c;
-        const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + c;
-        a.partial[base] = 0.0f;
-        a.partial[base + a.N] = 0.0f;
-        if (kGh5) {
-          a.variances[base] = 0.0f;
-          a.variances[base + a.N] = 0.0f;
-        }
-        a.scores[flat] = cfm_score(0.0f, 0.0f, 0.0f, 0.0f, 0.0f, a.weights[t * a.K + k], 0.0f,
-                                   0.0f, a.gelu != 0, a.point != 0);
-      }
-    }
+    if (t < a.T) score_absent_slots<kGh5>(a, t, kFusedThreads);
     return;
   }
   const int z = blockIdx.x / a.channel_groups;
@@ -1228,77 +1262,6 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
   }
   *reinterpret_cast<float4 *>(a.scores + static_cast<long>(token) * a.N + static_cast<long>(slot) * a.I + c) =
       make_float4(score[0], score[1], score[2], score[3]);
-}
-
-// ---------------------------------------------------------------------------
-// score (progressive.py:1111-1353): split sums in split order, then the score
-
-struct ScoreArgs {
-  const float *parts;
-  const float *vparts;
-  const int32_t *ids;
-  const float *weights;
-  const uint8_t *padding;
-  const float *norms;
-  const float *geometry;
-  float *partial;
-  float *variances;
-  float *scores;
-  uint8_t *completed;
-  uint8_t *selected;
-  uint32_t *tile_masks;  // cleared here for the select kernel's channel masks (or NULL)
-  long mask_words;
-  int I, K, N, splits;
-  int gh5, gelu, point;
-};
-
-__global__ __launch_bounds__(256) void score_kernel(ScoreArgs a) {
-  const int logical = blockIdx.x * 256 + threadIdx.x;
-  const int t = blockIdx.y;
-  if (logical >= a.N) return;
-  // tokens * N >= tiles * I: every mask word has a thread
-  if (a.tile_masks && static_cast<long>(t) * a.N + logical < a.mask_words)
-    a.tile_masks[static_cast<long>(t) * a.N + logical] = 0u;
-  const int k = logical / a.I, c = logical % a.I;
-  const long stride = 2l * a.N;
-  const long base = static_cast<long>(t) * a.splits * stride + logical;
-  const int e = a.ids[t * a.K + k];
-  const bool local = is_active(a.padding, t) && e >= 0;
-  // padding rows and absent experts are screened by no workgroup: zero
-  float g = 0.0f, u = 0.0f, vg = 0.0f, vu = 0.0f;
-  if (local) {
-    g = a.parts[base];
-    u = a.parts[base + a.N];
-    if (a.gh5) {
-      vg = a.vparts[base];
-      vu = a.vparts[base + a.N];
-    }
-    for (int s = 1; s < a.splits; ++s) {
-      g = g + a.parts[base + s * stride];
-      u = u + a.parts[base + s * stride + a.N];
-      if (a.gh5) {
-        vg = vg + a.vparts[base + s * stride];
-        vu = vu + a.vparts[base + s * stride + a.N];
-      }
-    }
-  }
-  const long address = static_cast<long>(t) * stride + logical;
-  a.partial[address] = g;
-  a.partial[address + a.N] = u;
-  if (a.gh5) {
-    a.variances[address] = vg;
-    a.variances[address + a.N] = vu;
-  }
-  const float norm = local ? a.norms[static_cast<long>(e) * a.I + c] : 0.0f;
-  float alpha = 0.0f, beta = 0.0f;
-  if (local && a.geometry) {
-    alpha = a.geometry[(static_cast<long>(e) * a.I + c) * 2];
-    beta = a.geometry[(static_cast<long>(e) * a.I + c) * 2 + 1];
-  }
-  const long flat = static_cast<long>(t) * a.N + logical;
-  a.scores[flat] = cfm_score(g, u, vg, vu, norm, a.weights[t * a.K + k], alpha, beta,
-                             a.gelu != 0, a.point != 0);
-  a.selected[flat] = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1728,10 +1691,12 @@ __global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
   const int f = blockIdx.x * 4 + wave;
   const int t = blockIdx.y;
   if (f >= a.F) return;
-  const int logical = a.next_ids[static_cast<long>(t) * a.F + f];
+  // the kept id and the token's expert ids in one round trip (lane k: slot k)
+  const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
+  const int logical = __builtin_amdgcn_readfirstlane(load_global(a.next_ids + static_cast<long>(t) * a.F + f));
   if (logical < 0 || logical >= a.N) return;
   const int k = logical / a.I, c = logical % a.I;
-  const int e = a.ids[t * a.K + k];
+  const int e = __builtin_amdgcn_readlane(slot_id, k);
   const bool active = is_active(a.padding, t);
   float g = 0.0f, u = 0.0f;
   if (e >= 0) {
@@ -2481,8 +2446,6 @@ int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *siz
       cap * s.B * 4,                          // norm2
       cap * 2 * n * 4,                        // partial
       cap * 2 * n * 4,                        // variances
-      cap * s.splits * 2 * n * 4,             // screen_parts
-      cap * s.splits * 2 * n * 4,             // screen_variance_parts
       cap * n * 4,                            // scores
       cap * s.F * 4,                          // next_ids
       cap * n,                                // selected
@@ -2560,10 +2523,6 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   if (!weights || !workspace || !hidden || !router_ids || !router_weights || !out)
     return fail(CFMOE_EINVAL, "NULL argument");
   if (tokens < 1 || tokens > workspace->capacity) return fail(CFMOE_EINVAL, "tokens out of range");
-  // the screen writes its split partials with 16-byte stores
-  if ((reinterpret_cast<uintptr_t>(workspace->screen_parts) |
-       reinterpret_cast<uintptr_t>(workspace->screen_variance_parts)) % 16)
-    return fail(CFMOE_EINVAL, "screen_parts and screen_variance_parts must be 16-byte aligned");
   const Shape s = shape_of(dims);
   if (tokens * s.K > kMaxPairs) return fail(CFMOE_EINVAL, "tokens * top_k exceeds 8192 pairs");
   if (s.R > 0 && (!weights->encoder_t || !weights->decoder))
@@ -2620,46 +2579,17 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   sel.union_row_bytes = 4.0 * s.H;
 
   if (s.screened) {
-    GroupScreenArgs sc;
-    sc.planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
-    sc.stats = static_cast<const uint16_t *>(weights->statistics);
-    sc.coords = workspace->coordinates;
-    sc.qvals = workspace->qvals;
-    sc.qexp = workspace->qexp;
-    sc.qsums = workspace->qsums;
-    sc.norm2 = workspace->norm2;
-    sc.group_experts = workspace->group_experts;
-    sc.group_starts = workspace->group_starts;
-    sc.group_counts = workspace->group_counts;
-    sc.group_pairs = workspace->group_pairs;
-    sc.group_total = workspace->group_total;
-    sc.parts = workspace->screen_parts;
-    sc.vparts = workspace->screen_variance_parts;
-    sc.H = s.H;
-    sc.I = s.I;
-    sc.K = s.K;
-    sc.N = s.N;
-    sc.keep = s.keep;
-    sc.splits = s.splits;
-    sc.span = s.span;
-    // (tile, split) segments, each cut into parts of row tiles so that about
-    // four workgroups per CU are live; a part keeps at least one row tile per
-    // wave. Workgroups of tiles past the device's tile count exit at once.
-    const long segments = tile_bound(tokens, s.K, dims->experts) * s.splits;
-    const int row_tiles = 2 * s.I / kRowTile;
-    const long target = 4L * compute_units();
-    long parts = (target + segments - 1) / segments;
-    parts = std::max(1L, std::min(parts, static_cast<long>((row_tiles + 3) / 4)));
-    sc.tiles_per_part = static_cast<int>((row_tiles + parts - 1) / parts);
-    sc.parts_per_segment = (row_tiles + sc.tiles_per_part - 1) / sc.tiles_per_part;
-    const long items = segments * sc.parts_per_segment;
-    // grouped batches: the fused screen and score (no split partials, no
-    // score launch); smaller ones split the blocks over more workgroups
-    const bool fused = grouped;
-    if ((stages & (1u << CFMOE_STAGE_SCREEN)) && fused) {
+    const uint2 *trit_planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
+    const uint16_t *statistics = static_cast<const uint16_t *>(weights->statistics);
+    const long tiles = tile_bound(tokens, s.K, dims->experts);
+    // grouped batches: the fused screen (every split of a channel tile in one
+    // wave); smaller ones: a workgroup per channel tile whose waves share the
+    // splits. Both score in place; workgroups of tiles past the device's tile
+    // count exit at once, and one workgroup per token writes absent slots.
+    if ((stages & (1u << CFMOE_STAGE_SCREEN)) && grouped) {
       FusedScreenArgs fs;
-      fs.planes = sc.planes;
-      fs.stats = sc.stats;
+      fs.planes = trit_planes;
+      fs.stats = statistics;
       fs.digits = workspace->digits;
       fs.qexp = workspace->qexp;
       fs.qsums = workspace->qsums;
@@ -2685,7 +2615,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       fs.splits = s.splits;
       fs.span = s.span;
       fs.channel_groups = (s.I / kRowTile + kFusedWaves - 1) / kFusedWaves;
-      fs.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * fs.channel_groups;
+      fs.tile_items = static_cast<int>(tiles) * fs.channel_groups;
       fs.gelu = gelu;
       fs.point = !gh5;
       const unsigned blocks = static_cast<unsigned>(fs.tile_items + tokens);
@@ -2695,42 +2625,46 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
         hipLaunchKernelGGL(fused_screen_kernel<false>, dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
       if ((rc = check_launch("screen"))) return rc;
     } else if (stages & (1u << CFMOE_STAGE_SCREEN)) {
+      SmallScreenArgs ss;
+      ss.planes = trit_planes;
+      ss.stats = statistics;
+      ss.digits = workspace->digits;
+      ss.qexp = workspace->qexp;
+      ss.qsums = workspace->qsums;
+      ss.norm2 = workspace->norm2;
+      ss.group_experts = workspace->group_experts;
+      ss.group_counts = workspace->group_counts;
+      ss.group_pairs = workspace->group_pairs;
+      ss.group_total = workspace->group_total;
+      ss.ids = workspace->ids;
+      ss.weights = workspace->weights;
+      ss.padding = padding;
+      ss.norms = weights->norms;
+      ss.geometry = (flags & CFMOE_GEOMETRY) ? weights->geometry : nullptr;
+      ss.partial = workspace->partial;
+      ss.variances = workspace->variances;
+      ss.scores = workspace->scores;
+      ss.H = s.H;
+      ss.I = s.I;
+      ss.K = s.K;
+      ss.N = s.N;
+      ss.T = tokens;
+      ss.splits = s.splits;
+      ss.span = s.span;
+      ss.tile_items = static_cast<int>(tiles) * (s.I / kRowTile);
+      // a tile holds at most 16 pairs, and at most tokens * K
+      ss.max_pairs = static_cast<int>(std::min<long>(kPairTile, static_cast<long>(tokens) * s.K));
+      ss.gelu = gelu;
+      ss.point = !gh5;
+      const unsigned blocks = static_cast<unsigned>(ss.tile_items + tokens);
+      const unsigned lds = static_cast<unsigned>(small_screen_lds(ss.max_pairs));
       if (gh5)
-        hipLaunchKernelGGL(group_screen_kernel<true>, dim3(static_cast<unsigned>(items)),
-                           dim3(256), 0, stream, sc);
+        hipLaunchKernelGGL(small_screen_kernel<true>, dim3(blocks), dim3(64 * kSmallWaves), lds, stream, ss);
       else
-        hipLaunchKernelGGL(group_screen_kernel<false>, dim3(static_cast<unsigned>(items)),
-                           dim3(256), 0, stream, sc);
+        hipLaunchKernelGGL(small_screen_kernel<false>, dim3(blocks), dim3(64 * kSmallWaves), lds, stream, ss);
       if ((rc = check_launch("screen"))) return rc;
     }
 
-    ScoreArgs so;
-    so.parts = workspace->screen_parts;
-    so.vparts = workspace->screen_variance_parts;
-    so.ids = workspace->ids;
-    so.weights = workspace->weights;
-    so.padding = padding;
-    so.norms = weights->norms;
-    so.geometry = (flags & CFMOE_GEOMETRY) ? weights->geometry : nullptr;
-    so.partial = workspace->partial;
-    so.variances = workspace->variances;
-    so.scores = workspace->scores;
-    so.completed = workspace->completed;
-    so.selected = workspace->selected;
-    so.I = s.I;
-    so.K = s.K;
-    so.N = s.N;
-    so.splits = s.splits;
-    so.gh5 = gh5;
-    so.gelu = gelu;
-    so.point = !gh5;
-    so.tile_masks = sel.tile_masks;
-    so.mask_words = tile_bound(tokens, s.K, dims->experts) * s.I;
-    if ((stages & (1u << CFMOE_STAGE_SCORE)) && !fused) {
-      hipLaunchKernelGGL(score_kernel, dim3((s.N + 255) / 256, tokens), dim3(256), 0, stream,
-                         so);
-      if ((rc = check_launch("score"))) return rc;
-    }
     if (stages & (1u << CFMOE_STAGE_SELECT)) {
       if (s.N <= 8 * kSelectThreads)
         hipLaunchKernelGGL(select_kernel<8>, dim3(tokens), dim3(kSelectThreads), 0, stream, sel);
@@ -3033,8 +2967,6 @@ int cfmoe_forward_noalloc(const cfmoe_dims *dims, const cfmoe_weights *weights,
       reinterpret_cast<void **>(&ws.qvals), reinterpret_cast<void **>(&ws.qexp),
       reinterpret_cast<void **>(&ws.qsums), reinterpret_cast<void **>(&ws.norm2),
       reinterpret_cast<void **>(&ws.partial), reinterpret_cast<void **>(&ws.variances),
-      reinterpret_cast<void **>(&ws.screen_parts),
-      reinterpret_cast<void **>(&ws.screen_variance_parts),
       reinterpret_cast<void **>(&ws.scores), reinterpret_cast<void **>(&ws.next_ids),
       reinterpret_cast<void **>(&ws.selected), reinterpret_cast<void **>(&ws.completed),
       reinterpret_cast<void **>(&ws.activations), reinterpret_cast<void **>(&ws.starts),

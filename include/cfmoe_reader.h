@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 7
+#define CFMOE_ABI_VERSION 8
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -50,10 +50,9 @@ typedef struct ihipStream_t *cfmoe_stream;
 
 /* Stages of one call, in launch order (cfmoe_launch_stage). */
 #define CFMOE_STAGE_PREPARE 0 /* route, rotate, mask, grid quantisation */
-#define CFMOE_STAGE_SCREEN 1  /* sketch projections per block split; in grouped calls
-                                 also the split sums and channel scores */
-#define CFMOE_STAGE_SCORE 2   /* split sums and channel scores (launches nothing in
-                                 grouped calls) */
+#define CFMOE_STAGE_SCREEN 1  /* sketch projections and the channel scores */
+#define CFMOE_STAGE_SCORE 2   /* split sums and channel scores (launches nothing: the
+                                 screen launch scores) */
 #define CFMOE_STAGE_SELECT 3  /* per-token top-F */
 #define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels (and the encoder, below) */
 #define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels; below the grouped
@@ -99,8 +98,8 @@ typedef struct cfmoe_weights {
 /* Caller-allocated scratch, sized for `capacity` tokens (sizes in bytes from
  * cfmoe_workspace_sizes). Layouts match the reference workspace
  * (progressive.py:2868-3121) where the Python operator exposes them. Every
- * buffer is 16-byte aligned (checked for the screen partials, which take
- * 16-byte stores). */
+ * buffer is 16-byte aligned (checked for the projections, variances, scores,
+ * digits and norms, which take 16-byte accesses). */
 typedef struct cfmoe_workspace {
   int32_t capacity;
   int32_t *ids;               /* [cap, K] sorted local expert ids */
@@ -113,8 +112,6 @@ typedef struct cfmoe_workspace {
   float *norm2;               /* [cap, B] squared norm of kept values */
   float *partial;             /* [cap, 2, N] gate/up projections */
   float *variances;           /* [cap, 2, N] */
-  float *screen_parts;        /* [cap, S, 2, N] split partial projections */
-  float *screen_variance_parts; /* [cap, S, 2, N] */
   float *scores;              /* [cap, N] */
   int32_t *next_ids;          /* [cap, F] kept candidate ids, ascending */
   uint8_t *selected;          /* [cap, N] */
@@ -142,7 +139,7 @@ typedef struct cfmoe_workspace {
 } cfmoe_workspace;
 
 /* Byte sizes of every workspace buffer, in struct order after `capacity`
- * (33 entries, read_work excluded). Returns the number written. */
+ * (31 entries, read_work excluded). Returns the number written. */
 CFMOE_API int cfmoe_workspace_sizes(const cfmoe_dims *dims, int32_t capacity, int64_t *sizes,
                           int32_t count);
 

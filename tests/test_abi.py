@@ -54,15 +54,20 @@ def test_forward_rejects_null_arguments_without_touching_a_device():
     assert b"NULL" in lib.cfmoe_last_error()
 
 
-def test_forward_rejects_misaligned_screen_partials_without_touching_a_device():
+def test_forward_rejects_misaligned_projections_without_touching_a_device():
     lib = _ext.library()
     dims = _ext.Dims(256, 64, 2, 4, 0, 16, 80, 0)
     weights = _ext.WeightPointers()
+    weights.trit_planes = 0x4000
+    weights.statistics = 0x5000
+    weights.norms = 0x6000
     workspace = _ext.WorkspacePointers()
     workspace.capacity = 1
-    workspace.screen_parts = 0x1000 + 4
-    workspace.screen_variance_parts = 0x2000
-    fake = ctypes.c_void_p(0x3000)
+    workspace.partial = 0x1000 + 4
+    workspace.variances = 0x2000
+    workspace.scores = 0x3000
+    workspace.digits = 0x7000
+    fake = ctypes.c_void_p(0x8000)
     status = lib.cfmoe_forward(ctypes.byref(dims), ctypes.byref(weights),
                                ctypes.byref(workspace), fake, fake, fake, None, fake, 1,
                                None, None)
