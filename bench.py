@@ -153,7 +153,7 @@ def algorithmic_bytes(reader: ProgressiveReader, tokens: int) -> dict[str, int]:
 
 STAGE_BYTES = {"screen": ("sketch",), "exact": ("gate_up",), "down": ("down",),
                "encode": ("encoder",)}
-DIRECT_RANK = 32  # rank at which grouped batches run the encoder inside the exact launch
+DIRECT_RANK = 32  # rank at which the encoder runs inside the exact launch
 STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "small_screen_kernel",
                  "select": "select_kernel", "exact": "exact_kernel",
                  "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
@@ -163,7 +163,7 @@ GROUP_EXACT_TOKENS = GROUPED_TOKENS  # batches from which the exact stage runs g
 def encoder_in_exact(tokens: int, rank: int) -> bool:
     """Whether the exact launch also runs the recovery encoder (the encode
     stage then launches nothing)."""
-    return rank > 0 and (tokens < GROUP_EXACT_TOKENS or rank == DIRECT_RANK)
+    return rank == DIRECT_RANK
 
 
 def stage_bytes(stage: str, tokens: int, rank: int) -> tuple[str, ...]:

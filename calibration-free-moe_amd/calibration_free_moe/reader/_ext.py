@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 POINT = 1
 GELU = 2

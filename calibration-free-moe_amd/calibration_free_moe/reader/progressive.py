@@ -989,11 +989,9 @@ class ProgressiveReader:
             "grouped_rows": grouped_rows,
             "grouped_issued_matrix_macs": grouped_macs,
             "workspace_bytes": float(self.workspace_bytes),
-            # below the grouped size the exact launch stages encoder rows in LDS
-            "batch_one_completion_shared_bytes_per_cta_upper_bound": float(
-                4 * 64 * 2 * (-(-self.rank // 8) * 8 + 8)
-            )
-            * (self.rank > 0),
+            # the exact rows use no LDS below the grouped size (one wave per
+            # kept channel; the encoder's rank-32 rows stay in registers)
+            "batch_one_completion_shared_bytes_per_cta_upper_bound": 0.0,
             "small_batch_recovery_counter_io_bytes_per_token": 0.0,
             "small_batch_recovery_counter_sector_bytes_per_token_upper_bound": 0.0,
             "small_batch_radix_scratch_io_bytes_per_token_upper_bound": 0.0,

@@ -12,8 +12,12 @@
 //   fused_screen_kernel  the same for grouped batches: every split of a
 //                    channel tile in one wave             (:2428-2606)
 //   select_kernel    per-token top-F (radix select + compaction) (:1584-1775)
-//   exact_kernel     native gate/up rows of kept channels         (:1372-1581)
+//   exact_kernel     native gate/up rows of kept channels, batches below
+//                    the grouped size: a wave per channel         (:1372-1581)
+//   group_exact_kernel  grouped batches: gate/up rows of the channels some
+//                    pair of an expert tile kept, read once per tile (:2655-2718)
 //   encode_kernel    recovery encoder over skipped channels       (:1859-2016)
+//                    (at rank 32 it runs inside the exact launches)
 //   down_kernel      down rows of kept channels, 32-channel tiles (:1778-1856)
 //   output_kernel    latent, decoder correction, router mix       (:2019-2111)
 //
@@ -1571,11 +1575,6 @@ __device__ __forceinline__ void encode_tile(const EncodeArgs &a, int tile, int k
     a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * a.R + lane] = acc;
 }
 
-// LDS row stride (bf16) of a wave's staged encoder rows when encode runs
-// inside the exact kernels (sized by R: the exact workgroups share the launch)
-__host__ __device__ inline int encode_stride(int R) { return (R + 7) / 8 * 8 + 8; }
-constexpr int kEncodeWaves = 4;  // encode items per 256-thread workgroup of the exact kernels
-
 __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   __shared__ __align__(16) uint16_t coefficients[64 * kEncodeStride];
   encode_tile(a, blockIdx.x, blockIdx.y, blockIdx.z, true, coefficients, kEncodeStride);
@@ -1646,101 +1645,12 @@ __device__ __forceinline__ void encode_tile_direct(const Args &a, int tile, int 
   if (half == 1) a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * R + r] = acc;
 }
 
-// ---------------------------------------------------------------------------
-// exact (progressive.py:1510-1546): one wave per kept channel
-
-struct ExactArgs {
-  const uint16_t *gate_up;
-  const uint16_t *x;
-  const int32_t *ids;
-  const uint8_t *padding;
-  const int32_t *next_ids;
-  float *partial;
-  uint16_t *activations;
-  uint8_t *completed;
-  int H, I, K, N, F, gelu;
-  // encode items run by the workgroups past exact_blocks (0: none); encode
-  // reads no exact result (a skipped channel is never completed)
-  EncodeArgs encode;
-  int exact_blocks, encode_items;
-};
-
-// Workgroups of an exact kernel past its own work run four encode items
-// (one per wave) from the launch's dynamic LDS.
-// `item` enumerates (tile, slot, token) tile-fastest; a wave past the work
-// runs a valid (clamped) item and stores nothing.
-__device__ __forceinline__ void encode_in_exact(const EncodeArgs &enc, int item, bool store) {
-  extern __shared__ __align__(16) uint16_t encode_lds[];
-  const int wave = threadIdx.x >> 6;
-  const int stride = encode_stride(enc.R);
-  const int tile = item % enc.tiles, rest = item / enc.tiles;
-  const int k = rest % enc.K, t = rest / enc.K;
-  encode_tile(enc, tile, k, t, store, encode_lds + wave * 64 * stride, stride);
-}
-
-__global__ __launch_bounds__(256) void exact_kernel(ExactArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (static_cast<int>(blockIdx.x) >= a.exact_blocks) {
-    // this token's encode items
-    const int per_token = a.encode.tiles * a.encode.K;
-    const int local_item = (blockIdx.x - a.exact_blocks) * kEncodeWaves + wave;
-    encode_in_exact(a.encode, blockIdx.y * per_token + min(local_item, per_token - 1),
-                    local_item < per_token);
-    return;
-  }
-  const int f = blockIdx.x * 4 + wave;
-  const int t = blockIdx.y;
-  if (f >= a.F) return;
-  // the kept id and the token's expert ids in one round trip (lane k: slot k)
-  const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
-  const int logical = __builtin_amdgcn_readfirstlane(load_global(a.next_ids + static_cast<long>(t) * a.F + f));
-  if (logical < 0 || logical >= a.N) return;
-  const int k = logical / a.I, c = logical % a.I;
-  const int e = __builtin_amdgcn_readlane(slot_id, k);
-  const bool active = is_active(a.padding, t);
-  float g = 0.0f, u = 0.0f;
-  if (e >= 0) {
-    const uint16_t *grow = a.gate_up + (static_cast<long>(e) * 2 * a.I + c) * a.H;
-    const uint16_t *urow = grow + static_cast<long>(a.I) * a.H;
-    const uint16_t *xr = a.x + static_cast<long>(t) * a.H;
-    for (int j = 0; 512 * j < a.H; ++j) {
-      const int h = 512 * j + 8 * lane;
-      if (h >= a.H) continue;
-      const uint4 gw = load_stream16(grow + h);
-      const uint4 uw = load_stream16(urow + h);
-      uint4 xw = make_uint4(0, 0, 0, 0);
-      if (active) xw = *reinterpret_cast<const uint4 *>(xr + h);
-      const uint32_t gv[4] = {gw.x, gw.y, gw.z, gw.w};
-      const uint32_t uv[4] = {uw.x, uw.y, uw.z, uw.w};
-      const uint32_t xv[4] = {xw.x, xw.y, xw.z, xw.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
-        g = fmaf(__uint_as_float(gv[i] << 16), x0, g);
-        g = fmaf(__uint_as_float(gv[i] & 0xffff0000u), x1, g);
-        u = fmaf(__uint_as_float(uv[i] << 16), x0, u);
-        u = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, u);
-      }
-    }
-    g = wave_sum_lane0(g);
-    u = wave_sum_lane0(u);
-  }
-  if (lane == 0) {
-    const long address = static_cast<long>(t) * 2 * a.N + logical;
-    a.partial[address] = g;
-    a.partial[address + a.N] = u;
-    const float act = bfr(cfm_activate(bfr(g), a.gelu != 0));
-    a.activations[static_cast<long>(t) * a.N + logical] = f2bf(act * bfr(u));
-    a.completed[static_cast<long>(t) * a.N + logical] = 1;
-  }
-}
-
 // Grouped exact rows (batches of grouped_tokens or more, as
 // progressive.py:2655-2718): wave = (16-pair expert tile, channel). The
 // select kernel's tile mask names the tile's pairs that kept the channel; it
 // and the tile's pairs (16 slots per tile) are read together. If any pair
 // kept the channel, its gate and up rows are read once and dotted with each
-// such pair's hidden row in the lane order of exact_kernel (identical results).
+// such pair's hidden row in the lane order of row_dots (identical results).
 // Workgroups past the tiles (one per token) write the zero results of padded
 // tokens and non-local slots, which the grouping leaves out.
 struct GroupExactArgs {
@@ -1778,6 +1688,35 @@ struct GroupExactArgs {
 
 constexpr int kMaxHidden = 2048;
 constexpr int kDownBuilders = 8;  // one per XCD
+constexpr int kHiddenParts = kMaxHidden / 512;  // 16-byte parts per lane of a hidden-size row
+
+// Lane-ordered gate and up dots with a hidden row, each row held as
+// kHiddenParts 16-byte parts per lane (part j of lane l: h = 512 j + 8 l + i,
+// i < 8): the lane's partial sums in h order; parts past H leave them
+// untouched. Every exact row of the reader is this chain, then wave_sum_lane0.
+__device__ __forceinline__ void row_dots(const uint4 (&gw)[kHiddenParts],
+                                         const uint4 (&uw)[kHiddenParts],
+                                         const uint4 (&xw)[kHiddenParts], int H, int lane,
+                                         float &g, float &u) {
+#pragma unroll
+  for (int j = 0; j < kHiddenParts; ++j) {
+    const bool inside = 512 * j + 8 * lane < H;
+    const uint32_t gv[4] = {gw[j].x, gw[j].y, gw[j].z, gw[j].w};
+    const uint32_t uv[4] = {uw[j].x, uw[j].y, uw[j].z, uw[j].w};
+    const uint32_t xv[4] = {xw[j].x, xw[j].y, xw[j].z, xw[j].w};
+    float gj = g, uj = u;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
+      gj = fmaf(__uint_as_float(gv[i] << 16), x0, gj);
+      gj = fmaf(__uint_as_float(gv[i] & 0xffff0000u), x1, gj);
+      uj = fmaf(__uint_as_float(uv[i] << 16), x0, uj);
+      uj = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, uj);
+    }
+    g = inside ? gj : g;
+    u = inside ? uj : u;
+  }
+}
 
 // Builder x of the down kernel's workgroup order. Workgroup b of the down
 // launch runs on XCD b % 8, in the order b / 8 there; entry 8 r + x of the
@@ -1957,7 +1896,7 @@ group_exact_kernel(GroupExactArgs a) {
   const __amdgpu_buffer_rsrc_t gate_rows = buffer_resource(a.gate_up + grow, row_bytes);
   const __amdgpu_buffer_rsrc_t up_rows =
       buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
-  constexpr int kParts = kMaxHidden / 512;
+  constexpr int kParts = kHiddenParts;
   uint4 xw[kParts];
   auto load_hidden = [&](int pp) {
     const int t = __builtin_amdgcn_readlane(token, pp);
@@ -1997,24 +1936,7 @@ group_exact_kernel(GroupExactArgs a) {
     for (int j = 0; j < kParts; ++j)
       asm volatile("" : "+v"(gw[j].x), "+v"(gw[j].y), "+v"(gw[j].z), "+v"(gw[j].w),
                    "+v"(uw[j].x), "+v"(uw[j].y), "+v"(uw[j].z), "+v"(uw[j].w));
-#pragma unroll
-    for (int j = 0; j < kParts; ++j) {
-      const bool inside = 512 * j + 8 * lane < a.H;
-      const uint32_t gv[4] = {gw[j].x, gw[j].y, gw[j].z, gw[j].w};
-      const uint32_t uv[4] = {uw[j].x, uw[j].y, uw[j].z, uw[j].w};
-      const uint32_t xv[4] = {xw[j].x, xw[j].y, xw[j].z, xw[j].w};
-      float gj = g, uj = uu;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x0 = __uint_as_float(xv[i] << 16), x1 = __uint_as_float(xv[i] & 0xffff0000u);
-        gj = fmaf(__uint_as_float(gv[i] << 16), x0, gj);
-        gj = fmaf(__uint_as_float(gv[i] & 0xffff0000u), x1, gj);
-        uj = fmaf(__uint_as_float(uv[i] << 16), x0, uj);
-        uj = fmaf(__uint_as_float(uv[i] & 0xffff0000u), x1, uj);
-      }
-      g = inside ? gj : g;
-      uu = inside ? uj : uu;
-    }
+    row_dots(gw, uw, xw, a.H, lane, g, uu);
     g = wave_sum_lane0(g);
     uu = wave_sum_lane0(uu);
     kept_g = lane == pp ? g : kept_g;
@@ -2044,8 +1966,57 @@ constexpr int kDownOutputs = 8;  // outputs per down thread (H / 8 threads)
 
 typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 
-// Workgroup per (32-channel tile, token), H / 4 threads of four outputs each.
-// Every wave works alone (no LDS, no barrier): the token's slot records
+// The slot of a token's down tile: the slot whose tiles hold it, the tile's
+// first position in the slot's kept list, and the slot's count, expert and
+// start in next_ids (k = -1: the tile is past the token's tiles).
+struct DownTile {
+  int k, first, count, e, start;
+};
+
+// At K = 8 the token's four records arrive through the scalar cache in one
+// round trip.
+__device__ __forceinline__ DownTile down_tile_slot(const int32_t *counts, const int32_t *tile_starts,
+                                                   const int32_t *ids, const int32_t *starts,
+                                                   int K, int t, int tile) {
+  DownTile d = {-1, 0, 0, -1, 0};
+  if (K == 8) {
+    const long row = static_cast<long>(t) * 8;
+    const i32x8 c8 = load_uniform(reinterpret_cast<const i32x8 *>(counts + row));
+    const i32x8 t8 = load_uniform(reinterpret_cast<const i32x8 *>(tile_starts + row));
+    const i32x8 e8 = load_uniform(reinterpret_cast<const i32x8 *>(ids + row));
+    const i32x8 s8 = load_uniform(reinterpret_cast<const i32x8 *>(starts + row));
+    asm volatile("" ::"s"(c8), "s"(t8), "s"(e8), "s"(s8));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (tile >= t8[s] && tile < t8[s] + (c8[s] + kDownTile - 1) / kDownTile) {
+        d.k = s;
+        d.first = (tile - t8[s]) * kDownTile;
+        d.count = c8[s];
+        d.e = e8[s];
+        d.start = s8[s];
+      }
+    }
+  } else {
+    for (int s = 0; s < K; ++s) {
+      const int c = counts[t * K + s];
+      const int ts = tile_starts[t * K + s];
+      if (tile >= ts && tile < ts + (c + kDownTile - 1) / kDownTile) {
+        d.k = s;
+        d.first = (tile - ts) * kDownTile;
+        d.count = c;
+      }
+    }
+    if (d.k >= 0) {
+      d.e = ids[t * K + d.k];
+      d.start = starts[t * K + d.k];
+    }
+  }
+  return d;
+}
+
+// Workgroup per (32-channel tile, token) with H / 8 threads of eight outputs
+// each (grouped batches), or per (tile, token, 512 outputs) with one wave
+// (smaller batches: more CUs share a batch-1 call). Every wave works alone (no LDS, no barrier): the token's slot records
 // (counts, tile starts, ids, starts) come through the scalar cache in one
 // round trip, lanes l < 32 of the wave load the tile's channel id l (the tile
 // stops at the count or at the first invalid id, found by a ballot), the ids
@@ -2060,39 +2031,8 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
     tile = item % a.max_tiles;
     t = item / a.max_tiles;
   }
-  int k = -1, first = 0, count = 0, e = -1, start = 0;
-  if (a.K == 8) {
-    const long row = static_cast<long>(t) * 8;
-    const i32x8 counts = load_uniform(reinterpret_cast<const i32x8 *>(a.counts + row));
-    const i32x8 tiles = load_uniform(reinterpret_cast<const i32x8 *>(a.down_tile_starts + row));
-    const i32x8 ids = load_uniform(reinterpret_cast<const i32x8 *>(a.ids + row));
-    const i32x8 starts = load_uniform(reinterpret_cast<const i32x8 *>(a.starts + row));
-    asm volatile("" ::"s"(counts), "s"(tiles), "s"(ids), "s"(starts));
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (tile >= tiles[s] && tile < tiles[s] + (counts[s] + kDownTile - 1) / kDownTile) {
-        k = s;
-        first = (tile - tiles[s]) * kDownTile;
-        count = counts[s];
-        e = ids[s];
-        start = starts[s];
-      }
-    }
-  } else {
-    for (int s = 0; s < a.K; ++s) {
-      const int c = a.counts[t * a.K + s];
-      const int ts = a.down_tile_starts[t * a.K + s];
-      if (tile >= ts && tile < ts + (c + kDownTile - 1) / kDownTile) {
-        k = s;
-        first = (tile - ts) * kDownTile;
-        count = c;
-      }
-    }
-    if (k >= 0) {
-      e = a.ids[t * a.K + k];
-      start = a.starts[t * a.K + k];
-    }
-  }
+  const DownTile d = down_tile_slot(a.counts, a.down_tile_starts, a.ids, a.starts, a.K, t, tile);
+  const int k = d.k, first = d.first, count = d.count, e = d.e, start = d.start;
   if (k < 0 || tile >= a.max_tiles) return;
   const bool local = is_active(a.padding, t) && e >= 0;
   const int j = first + (lane & (kDownTile - 1));
@@ -2102,7 +2042,7 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   const uint32_t invalid = static_cast<uint32_t>(__ballot(!valid));
   const uint32_t live = invalid ? (1u << __builtin_ctz(invalid)) - 1u : 0xffffffffu;
   const int channel = valid ? logical % a.I : 0;
-  const int o = tid * kDownOutputs;
+  const int o = (blockIdx.z * blockDim.x + tid) * kDownOutputs;  // z: output chunk (per-token launch)
   const bool outputs = o < a.H;
   const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + min(o, a.H - 8);
   uint4 w[kDownTile];
@@ -2136,6 +2076,83 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   float *out = a.parts + (static_cast<long>(t) * a.max_tiles + tile) * a.H + o;
   *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
   *reinterpret_cast<float4 *>(out + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
+// ---------------------------------------------------------------------------
+// exact below the grouped size (progressive.py:1510-1546): one wave per kept
+// channel
+
+struct ExactArgs {
+  const uint16_t *gate_up;
+  const uint16_t *x;
+  const int32_t *ids;
+  const uint8_t *padding;
+  const int32_t *next_ids;
+  float *partial;
+  uint16_t *activations;
+  uint8_t *completed;
+  int H, I, K, N, F, gelu;
+  // recovery encoder items (R = kDirectRank) of the token, one per workgroup
+  // past exact_blocks (0: none); encode reads no exact result (a skipped
+  // channel is never completed)
+  EncodeArgs encode;
+  int exact_blocks, encode_items;
+};
+
+// Workgroup = one wave = kept channel f of token t: single-wave workgroups
+// spread a batch-1 call's rows over every CU. The kept id, the token's expert
+// ids and its padding flag arrive in one round trip, then the gate, up and
+// hidden rows with every part in flight (buffer resources: parts past H, and
+// a padded token's hidden row, read zeros); the chain is row_dots, as in
+// group_exact_kernel.
+__global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
+  const int lane = threadIdx.x;
+  const int t = blockIdx.y;
+  if (static_cast<int>(blockIdx.x) >= a.exact_blocks) {
+    const int item = blockIdx.x - a.exact_blocks;  // (tile, slot), tile fastest
+    if (item < a.encode_items)
+      encode_tile_direct(a.encode, item % a.encode.tiles, item / a.encode.tiles, t);
+    return;
+  }
+  const int f = blockIdx.x;
+  const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
+  const uint32_t padded = __builtin_amdgcn_raw_buffer_load_b8(
+      a.padding ? buffer_resource(a.padding, t + 1) : buffer_resource(a.ids, 0), t, 0, 0);
+  const int logical =
+      __builtin_amdgcn_readfirstlane(load_global(a.next_ids + static_cast<long>(t) * a.F + f));
+  asm volatile("" ::"v"(padded));  // the flag's load stays in this round trip
+  if (logical < 0 || logical >= a.N) return;
+  const int k = logical / a.I, c = logical % a.I;
+  const int e = __builtin_amdgcn_readlane(slot_id, k);
+  float g = 0.0f, u = 0.0f;
+  if (e >= 0) {
+    const bool active = __builtin_amdgcn_readfirstlane(padded) == 0;
+    const int row_bytes = 2 * a.H, offset = 16 * lane;
+    const long grow = (static_cast<long>(e) * 2 * a.I + c) * a.H;
+    const __amdgpu_buffer_rsrc_t gate_row = buffer_resource(a.gate_up + grow, row_bytes);
+    const __amdgpu_buffer_rsrc_t up_row =
+        buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
+    const __amdgpu_buffer_rsrc_t hidden =
+        buffer_resource(a.x + static_cast<long>(t) * a.H, active ? row_bytes : 0);
+    uint4 gw[kHiddenParts], uw[kHiddenParts], xw[kHiddenParts];
+#pragma unroll
+    for (int p = 0; p < kHiddenParts; ++p) {
+      xw[p] = buffer_load16(hidden, offset + 1024 * p);
+      gw[p] = buffer_stream16(gate_row, offset + 1024 * p);
+      uw[p] = buffer_stream16(up_row, offset + 1024 * p);
+    }
+    row_dots(gw, uw, xw, a.H, lane, g, u);
+    g = wave_sum_lane0(g);
+    u = wave_sum_lane0(u);
+  }
+  if (lane == 0) {
+    const long address = static_cast<long>(t) * 2 * a.N + logical;
+    a.partial[address] = g;
+    a.partial[address + a.N] = u;
+    const float act = bfr(cfm_activate(bfr(g), a.gelu != 0));
+    a.activations[static_cast<long>(t) * a.N + logical] = f2bf(act * bfr(u));
+    a.completed[static_cast<long>(t) * a.N + logical] = 1;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2695,127 +2712,120 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   en.R = s.R;
   en.tiles = s.encoder_tiles;
   en.gelu = gelu;
-  // Where the encoder runs inside the exact launch, the exact stage launches
-  // it (also alone, through cfmoe_launch_stage) and the encode stage has no
-  // launch of its own: small batches run it in the per-token exact launch (one
-  // launch fewer); grouped batches run it in the grouped exact launch when it
-  // needs no LDS (R = kDirectRank; the LDS encoder's dynamic LDS would apply to
-  // every exact workgroup and halve their occupancy)
-  const bool small = !grouped;
-  // grouped batches: the exact stage builds the down kernel's workgroup order
-  // (expert-grouped per XCD) and the down stage reads it
-  const bool down_order = !small;
+  // At R = kDirectRank the encoder runs inside the exact launch (it needs no
+  // LDS there), which the exact stage launches (also alone, through
+  // cfmoe_launch_stage); the encode stage then has no launch of its own.
+  // Grouped batches build the down kernel's workgroup order (expert-grouped
+  // per XCD) in the exact launch and read it in the down launch.
+  const bool encode_in_exact = s.R == kDirectRank;
+  const bool fuse_encode = encode_in_exact && (stages & (1u << CFMOE_STAGE_EXACT));
+  const int encode_items = fuse_encode ? s.encoder_tiles * s.K : 0;  // per token
   const int down_blocks = (tokens * s.max_tiles + 7) / 8 * 8;
-  const bool encode_in_exact = s.R > 0 && (small || s.R == kDirectRank);
-  const bool fuse_encode = encode_in_exact && small && (stages & (1u << CFMOE_STAGE_EXACT));
-  const bool fuse_direct = encode_in_exact && !small && (stages & (1u << CFMOE_STAGE_EXACT));
-  const int encode_items = fuse_encode ? s.encoder_tiles * s.K * tokens : 0;
-  const unsigned encode_lds =
-      fuse_encode ? static_cast<unsigned>(kEncodeWaves * 64 * encode_stride(s.R) * 2) : 0u;
-
-  ExactArgs ex;
-  ex.gate_up = static_cast<const uint16_t *>(weights->gate_up);
-  ex.x = static_cast<const uint16_t *>(hidden);
-  ex.ids = workspace->ids;
-  ex.padding = padding;
-  ex.next_ids = workspace->next_ids;
-  ex.partial = workspace->partial;
-  ex.activations = static_cast<uint16_t *>(workspace->activations);
-  ex.completed = workspace->completed;
-  ex.H = s.H;
-  ex.I = s.I;
-  ex.K = s.K;
-  ex.N = s.N;
-  ex.F = s.F;
-  ex.gelu = gelu;
-  if (stages & (1u << CFMOE_STAGE_EXACT)) {
-    if (grouped) {
-      GroupExactArgs gx;
-      gx.gate_up = ex.gate_up;
-      gx.x = ex.x;
-      gx.padding = padding;
-      gx.ids = workspace->ids;
-      gx.next_ids = workspace->next_ids;
-      gx.counts = workspace->counts;
-      gx.starts = workspace->starts;
-      gx.selected = workspace->selected;
-      gx.group_experts = workspace->group_experts;
-      gx.group_starts = workspace->group_starts;
-      gx.group_counts = workspace->group_counts;
-      gx.group_pairs = workspace->group_pairs;
-      gx.group_total = workspace->group_total;
-      gx.tile_masks = workspace->tile_masks;
-      gx.dense = s.screened ? 0 : 1;
-      gx.partial = workspace->partial;
-      gx.activations = ex.activations;
-      gx.completed = workspace->completed;
-      gx.H = s.H;
-      gx.I = s.I;
-      gx.K = s.K;
-      gx.N = s.N;
-      gx.F = s.F;
-      gx.T = tokens;
-      gx.gelu = gelu;
-      gx.channel_groups = (s.I + kGroupExactWaves - 1) / kGroupExactWaves;
-      gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
-      gx.encoder_t = en.encoder_t;
-      gx.parts = en.parts;
-      gx.tiles = en.tiles;
-      gx.encode_items = fuse_direct ? s.encoder_tiles * s.K * tokens : 0;
-      gx.down_order = workspace->down_order;
-      gx.pair_tiles = workspace->pair_tiles;
-      gx.down_tile_starts = workspace->down_tile_starts;
-      gx.max_tiles = s.max_tiles;
-      gx.down_blocks = down_blocks;
-      gx.order_words = static_cast<int>(down_list_words(workspace->capacity, s));
-      gx.slot_capacity = static_cast<int>(down_slot_capacity(workspace->capacity, s));
-      hipLaunchKernelGGL(group_exact_kernel,
-                         dim3(kDownBuilders + gx.tile_items + gx.encode_items + tokens),
-                         dim3(64 * kGroupExactWaves), 0, stream, gx);
-    } else {
-      ex.encode = en;
-      ex.encode_items = encode_items;
-      ex.exact_blocks = (s.F + 3) / 4;
-      const int encode_blocks =
-          fuse_encode ? (s.encoder_tiles * s.K + kEncodeWaves - 1) / kEncodeWaves : 0;
-      hipLaunchKernelGGL(exact_kernel, dim3(ex.exact_blocks + encode_blocks, tokens), dim3(256),
-                         encode_lds, stream, ex);
-    }
+  const uint16_t *gate_up = static_cast<const uint16_t *>(weights->gate_up);
+  const uint16_t *down = static_cast<const uint16_t *>(weights->down);
+  uint16_t *activations = static_cast<uint16_t *>(workspace->activations);
+  if ((stages & (1u << CFMOE_STAGE_EXACT)) && grouped) {
+    GroupExactArgs gx;
+    gx.gate_up = gate_up;
+    gx.x = static_cast<const uint16_t *>(hidden);
+    gx.padding = padding;
+    gx.ids = workspace->ids;
+    gx.next_ids = workspace->next_ids;
+    gx.counts = workspace->counts;
+    gx.starts = workspace->starts;
+    gx.selected = workspace->selected;
+    gx.group_experts = workspace->group_experts;
+    gx.group_starts = workspace->group_starts;
+    gx.group_counts = workspace->group_counts;
+    gx.group_pairs = workspace->group_pairs;
+    gx.group_total = workspace->group_total;
+    gx.tile_masks = workspace->tile_masks;
+    gx.dense = s.screened ? 0 : 1;
+    gx.partial = workspace->partial;
+    gx.activations = activations;
+    gx.completed = workspace->completed;
+    gx.H = s.H;
+    gx.I = s.I;
+    gx.K = s.K;
+    gx.N = s.N;
+    gx.F = s.F;
+    gx.T = tokens;
+    gx.gelu = gelu;
+    gx.channel_groups = (s.I + kGroupExactWaves - 1) / kGroupExactWaves;
+    gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
+    gx.encoder_t = en.encoder_t;
+    gx.parts = en.parts;
+    gx.tiles = en.tiles;
+    gx.encode_items = encode_items * tokens;
+    gx.down_order = workspace->down_order;
+    gx.pair_tiles = workspace->pair_tiles;
+    gx.down_tile_starts = workspace->down_tile_starts;
+    gx.max_tiles = s.max_tiles;
+    gx.down_blocks = down_blocks;
+    gx.order_words = static_cast<int>(down_list_words(workspace->capacity, s));
+    gx.slot_capacity = static_cast<int>(down_slot_capacity(workspace->capacity, s));
+    hipLaunchKernelGGL(group_exact_kernel,
+                       dim3(kDownBuilders + gx.tile_items + gx.encode_items + tokens),
+                       dim3(64 * kGroupExactWaves), 0, stream, gx);
+    if ((rc = check_launch("exact"))) return rc;
+  } else if (stages & (1u << CFMOE_STAGE_EXACT)) {
+    ExactArgs ex;
+    ex.gate_up = gate_up;
+    ex.x = static_cast<const uint16_t *>(hidden);
+    ex.ids = workspace->ids;
+    ex.padding = padding;
+    ex.next_ids = workspace->next_ids;
+    ex.partial = workspace->partial;
+    ex.activations = activations;
+    ex.completed = workspace->completed;
+    ex.H = s.H;
+    ex.I = s.I;
+    ex.K = s.K;
+    ex.N = s.N;
+    ex.F = s.F;
+    ex.gelu = gelu;
+    ex.encode = en;
+    ex.exact_blocks = s.F;
+    ex.encode_items = encode_items;
+    hipLaunchKernelGGL(exact_kernel, dim3(s.F + encode_items, tokens), dim3(kWave), 0, stream, ex);
     if ((rc = check_launch("exact"))) return rc;
   }
 
-  // otherwise (grouped batches at R != kDirectRank) it is its own kernel
   if (s.R > 0 && (stages & (1u << CFMOE_STAGE_ENCODE)) && !encode_in_exact) {
     hipLaunchKernelGGL(encode_kernel, dim3(s.encoder_tiles, s.K, tokens), dim3(64), 0, stream, en);
     if ((rc = check_launch("encode"))) return rc;
   }
 
-  DownArgs dn;
-  dn.down = static_cast<const uint16_t *>(weights->down);
-  dn.activations = static_cast<const uint16_t *>(workspace->activations);
-  dn.ids = workspace->ids;
-  dn.padding = padding;
-  dn.next_ids = workspace->next_ids;
-  dn.counts = workspace->counts;
-  dn.starts = workspace->starts;
-  dn.down_tile_starts = workspace->down_tile_starts;
-  dn.order = down_order ? workspace->down_order : nullptr;
-  dn.parts = workspace->down_parts;
-  dn.H = s.H;
-  dn.I = s.I;
-  dn.K = s.K;
-  dn.N = s.N;
-  dn.F = s.F;
-  dn.max_tiles = s.max_tiles;
-  const int down_threads = ((s.H / kDownOutputs + kWave - 1) / kWave) * kWave;
   if (stages & (1u << CFMOE_STAGE_DOWN)) {
-    if (down_order)
+    DownArgs dn;
+    dn.down = down;
+    dn.activations = activations;
+    dn.ids = workspace->ids;
+    dn.padding = padding;
+    dn.next_ids = workspace->next_ids;
+    dn.counts = workspace->counts;
+    dn.starts = workspace->starts;
+    dn.down_tile_starts = workspace->down_tile_starts;
+    dn.order = grouped ? workspace->down_order : nullptr;
+    dn.parts = workspace->down_parts;
+    dn.H = s.H;
+    dn.I = s.I;
+    dn.K = s.K;
+    dn.N = s.N;
+    dn.F = s.F;
+    dn.max_tiles = s.max_tiles;
+    const int down_threads = ((s.H / kDownOutputs + kWave - 1) / kWave) * kWave;
+    if (grouped) {
       hipLaunchKernelGGL(down_kernel, dim3(down_blocks), dim3(down_threads), 0, stream, dn);
-    else
-      hipLaunchKernelGGL(down_kernel, dim3(s.max_tiles, tokens), dim3(down_threads), 0, stream,
-                         dn);
+    } else {
+      // one wave per workgroup and 512 outputs each: a batch-1 call's tiles
+      // spread over H / 512 times as many CUs
+      hipLaunchKernelGGL(down_kernel, dim3(s.max_tiles, tokens, down_threads / kWave), dim3(kWave),
+                         0, stream, dn);
+    }
     if ((rc = check_launch("down"))) return rc;
   }
+
   if (!(stages & (1u << CFMOE_STAGE_OUTPUT))) return 0;
 
   OutputArgs op;

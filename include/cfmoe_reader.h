@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 8
+#define CFMOE_ABI_VERSION 9
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -54,10 +54,11 @@ typedef struct ihipStream_t *cfmoe_stream;
 #define CFMOE_STAGE_SCORE 2   /* split sums and channel scores (launches nothing: the
                                  screen launch scores) */
 #define CFMOE_STAGE_SELECT 3  /* per-token top-F */
-#define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels (and the encoder, below) */
-#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels; below the grouped
-                                 size and at rank 32 it runs inside the exact launch, and
-                                 this stage launches nothing */
+#define CFMOE_STAGE_EXACT 4   /* native gate/up rows of kept channels (and at rank 32 the
+                                 encoder) */
+#define CFMOE_STAGE_ENCODE 5  /* recovery encoder over skipped channels; at rank 32 it
+                                 runs inside the exact launch, and this stage launches
+                                 nothing */
 #define CFMOE_STAGE_DOWN 6    /* down rows of kept channels */
 #define CFMOE_STAGE_OUTPUT 7  /* latent, decoder correction, router mix */
 #define CFMOE_STAGE_COUNT 8
