@@ -1297,48 +1297,92 @@ constexpr int kSelectKeys = 16;  // keys per thread: N <= 16384
 // Histogram slot of a radix bin: one pad word per 32 bins, so that lanes
 // reading bins 32 apart use different LDS banks.
 __device__ __forceinline__ int select_slot(int bin) { return bin + (bin >> 5); }
-constexpr int kSelectSlots = 2048 + 2048 / 32;
 
-// The bin of a radix pass where the count of keys from the top reaches
-// `want`, found by one wave from the pass's histogram: lane l sums the
-// `per_lane` bins below bins - per_lane l, a wave scan finds the lane where
-// the running count reaches `want`, and its bins are scanned the same way,
-// one per lane. Returns the bin; *above receives the count of keys in higher
-// bins.
-__device__ __forceinline__ int select_find_bin(const int *histogram, int bins, int want,
-                                               int *above) {
+// Radix digits of the select passes: 12 and 12 bits, then the last 8 only
+// when the cutoff's 24-bit bin holds more keys than remain to be kept (else
+// every key of that bin is kept, whatever its low bits).
+constexpr int kSelectWideBins = 4096;
+constexpr int kSelectWideSlots = kSelectWideBins + kSelectWideBins / 32;
+constexpr int kSelectLastBins = 256;
+constexpr int kSelectLastSlots = kSelectLastBins + kSelectLastBins / 32;
+constexpr int kSelectWaves = kSelectThreads / kWave;
+constexpr int kSelectChunk = kSelectWideBins / kSelectWaves;  // bins per wave, 4 per lane
+
+// A pass's cutoff bin as every wave finds it, within the 64 kPer-bin lane
+// ranges below bin `top` (highest first): the first bin where `before` plus
+// the keys counted from `top` down reaches `want`, which the range holds.
+// Returns the bin; *above receives the keys in higher bins, *count the bin's.
+template <int kPer>
+__device__ __forceinline__ int select_scan(const int *histogram, int top, int want, int before,
+                                           int *above, int *count) {
   const int lane = threadIdx.x & 63;
-  const int per_lane = bins / kWave;
-  const int top = bins - lane * per_lane;
-  int mine = 0;
-#pragma unroll 8
-  for (int i = 1; i <= per_lane; ++i) mine += histogram[select_slot(top - i)];
-  const int inclusive = wave_inclusive(mine);
-  // want <= the keys left in the pass, so some lane reaches it
+  const int lane_top = top - lane * kPer;
+  int c[kPer], mine = 0;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    c[i] = histogram[select_slot(lane_top - 1 - i)];
+    mine += c[i];
+  }
+  const int inclusive = before + wave_inclusive(mine);
   const uint64_t reached = __ballot(inclusive >= want);
   const int owner = reached ? __builtin_ctzll(reached) : kWave - 1;
+  int running = __builtin_amdgcn_readlane(inclusive - mine, owner);
+  int bin = top - owner * kPer - kPer, at_above = running, at_count = 0;
+  bool found = false;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int ci = __builtin_amdgcn_readlane(c[i], owner);
+    if (!found && running + ci >= want) {
+      found = true;
+      bin = top - owner * kPer - 1 - i;
+      at_above = running;
+      at_count = ci;
+    }
+    running += ci;
+  }
+  *above = at_above;
+  *count = at_count;
+  return bin;
+}
+
+// The cutoff bin of a 4096-bin pass: wave w first sums its chunk of 256
+// bins (the w-th from the top) into totals[w]; after the barrier every wave
+// finds the chunk where the count reaches `want` from the 16 totals, then the
+// bin inside it (select_scan). No wave waits for another's result.
+__device__ __forceinline__ int select_wide(const int *histogram, int *totals, int want, int *above,
+                                           int *count) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunk_top = kSelectWideBins - kSelectChunk * wave - 4 * lane;
+  int sum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sum += histogram[select_slot(chunk_top - 1 - i)];
+  sum = wave_sum_all(sum);
+  if (lane == 0) totals[wave] = sum;
+  __syncthreads();
+  const int mine = lane < kSelectWaves ? totals[lane] : 0;
+  const int inclusive = wave_inclusive(mine);
+  const uint64_t reached = __ballot(lane < kSelectWaves && inclusive >= want);
+  const int owner = reached ? __builtin_ctzll(reached) : kSelectWaves - 1;
   const int before = __builtin_amdgcn_readlane(inclusive - mine, owner);
-  // the owner's bins, highest first, one per lane
-  const int owner_top = bins - owner * per_lane;
-  const int count = lane < per_lane ? histogram[select_slot(owner_top - 1 - lane)] : 0;
-  const int running = before + wave_inclusive(count);
-  const uint64_t hit = __ballot(lane < per_lane && running >= want);
-  const int at = hit ? __builtin_ctzll(hit) : per_lane - 1;
-  *above = __builtin_amdgcn_readlane(running - count, at);
-  return owner_top - 1 - at;
+  return select_scan<4>(histogram, kSelectWideBins - kSelectChunk * owner, want, before, above,
+                        count);
 }
 
 template <int kKeys>  // keys per thread: N <= kKeys * kSelectThreads
 __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
-  __shared__ int histogram[3][kSelectSlots];
+  __shared__ int wide[2][kSelectWideSlots];
+  __shared__ int last[kSelectLastSlots];
   __shared__ int scratch[32];
+  __shared__ int totals[kSelectWaves];
+  __shared__ int wave_totals[kSelectWaves];
   __shared__ int slot_start[65];
   __shared__ int slot_tiles[64];
-  __shared__ int shared_bin, shared_above;
-  __shared__ int union_scratch[kSelectThreads / kWave];
+  __shared__ int union_scratch[kSelectWaves];
   const int t = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
-  for (int i = tid; i < 3 * kSelectSlots; i += kSelectThreads) (&histogram[0][0])[i] = 0;
+  for (int i = tid; i < 2 * kSelectWideSlots; i += kSelectThreads) (&wide[0][0])[i] = 0;
+  if (tid < kSelectLastSlots) last[tid] = 0;
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
   // keys: every load issued unconditionally (absent keys read a zero)
@@ -1363,49 +1407,66 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   } else {
     __syncthreads();  // the histograms are zero
   }
-  // three radix passes (11/11/10 bits) find the want-th largest key; in each,
-  // wave 0 reads the bin off the LDS histogram between two barriers
+  // radix passes find the want-th largest key: `prefix` holds its known
+  // bits, `mask` which bits those are
   uint32_t prefix = 0, mask = 0;
   if (want > 0) {
-    const int shifts[3] = {21, 10, 0};
-    const int widths[3] = {11, 11, 10};
 #pragma unroll
-    for (int pass = 0; pass < 3; ++pass) {
-      const int shift = shifts[pass];
-      const uint32_t bins = 1u << widths[pass];
+    for (int pass = 0; pass < 2; ++pass) {
+      const int shift = pass == 0 ? 20 : 8;
 #pragma unroll
       for (int j = 0; j < kKeys; ++j)
         if (valid(j) && (key[j] & mask) == prefix)
-          atomicAdd(&histogram[pass][select_slot((key[j] >> shift) & (bins - 1))], 1);
+          atomicAdd(&wide[pass][select_slot((key[j] >> shift) & (kSelectWideBins - 1))], 1);
       __syncthreads();
-      if (tid < kWave) {
-        int above;
-        const int bin = select_find_bin(histogram[pass], static_cast<int>(bins), want, &above);
-        if (tid == 0) {
-          shared_bin = bin;
-          shared_above = above;
-        }
+      int above, count;
+      const int bin = select_wide(wide[pass], totals, want, &above, &count);
+      prefix |= static_cast<uint32_t>(bin) << shift;
+      mask |= static_cast<uint32_t>(kSelectWideBins - 1) << shift;
+      want -= above;
+      if (pass == 1 && count > want) {
+#pragma unroll
+        for (int j = 0; j < kKeys; ++j)
+          if (valid(j) && (key[j] & mask) == prefix)
+            atomicAdd(&last[select_slot(key[j] & (kSelectLastBins - 1))], 1);
+        __syncthreads();
+        const int low = select_scan<kSelectLastBins / kWave>(last, kSelectLastBins, want, 0,
+                                                              &above, &count);
+        prefix |= static_cast<uint32_t>(low);
+        mask = 0xffffffffu;
+        want -= above;
       }
-      __syncthreads();
-      prefix |= static_cast<uint32_t>(shared_bin) << shift;
-      mask |= (bins - 1) << shift;
-      want -= shared_above;
     }
   }
   const bool any = a.F > 0 && mask != 0;
-  // After the passes `prefix` is the cutoff key and `want` the ties it keeps.
-  // One scan of packed (above, tied) counts gives every thread the kept keys
-  // before it: all keys above the cutoff, ties in ascending candidate order.
+  // After the passes `prefix` is the cutoff key on the bits of `mask` and
+  // `want` the ties it keeps (all keys of the cutoff's bin when the last pass
+  // was skipped). One scan of packed (above, tied) counts gives every thread
+  // the kept keys before it: all keys above the cutoff, ties in ascending
+  // candidate order.
   const uint32_t cutoff = prefix;
   const int room = want;
+#pragma unroll
+  for (int j = 0; j < kKeys; ++j) key[j] &= mask;
   int above_here = 0, tied_here = 0;
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) {
     above_here += any && valid(j) && key[j] > cutoff;
     tied_here += any && valid(j) && key[j] == cutoff;
   }
-  int packed_total;
-  const int packed = block_exclusive(above_here | (tied_here << 16), scratch, &packed_total);
+  // exclusive prefix over threads (16-bit fields: at most N keys each), one
+  // barrier: the wave totals have an array of their own
+  const int packed_here = above_here | (tied_here << 16);
+  const int inclusive = wave_inclusive(packed_here);
+  if (lane == kWave - 1) wave_totals[wave] = inclusive;
+  __syncthreads();
+  int packed = inclusive - packed_here, packed_total = 0;
+#pragma unroll
+  for (int w = 0; w < kSelectWaves; ++w) {
+    const int v = wave_totals[w];
+    packed_total += v;
+    packed += w < wave ? v : 0;
+  }
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
   int above_before = packed & 0xffff, tied_before = packed >> 16;
   int union_rows = 0;  // (tile, channel) words this thread turned nonzero
@@ -1460,7 +1521,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __syncthreads();
   if (a.read_work && tid == 0) {
     int rows = 0;
-    for (int w = 0; w < kSelectThreads / kWave; ++w) rows += union_scratch[w];
+    for (int w = 0; w < kSelectWaves; ++w) rows += union_scratch[w];
     if (rows > 0) atomicAdd(a.read_work + 12, rows * a.union_row_bytes);
   }
   // wave 0: lane k writes slot k's count, start and tile starts (K <= 64)
