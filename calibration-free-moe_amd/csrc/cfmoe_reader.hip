@@ -1707,11 +1707,12 @@ __device__ __forceinline__ void encode_tile_direct(const Args &a, int tile, int 
 }
 
 // Grouped exact rows (batches of grouped_tokens or more, as
-// progressive.py:2655-2718): wave = (16-pair expert tile, channel). The
-// select kernel's tile mask names the tile's pairs that kept the channel; it
-// and the tile's pairs (16 slots per tile) are read together. If any pair
-// kept the channel, its gate and up rows are read once and dotted with each
-// such pair's hidden row in the lane order of row_dots (identical results).
+// progressive.py:2655-2718): wave = (16-pair expert tile, kExactChannels
+// channels). The select kernel's tile masks name the tile's pairs that kept
+// each channel; they and the tile's pairs (16 slots per tile) are read
+// together. For each channel some pair kept, in turn, its gate and up rows
+// are read once and dotted with each such pair's hidden row in the lane
+// order of row_dots (identical results).
 // Workgroups past the tiles (one per token) write the zero results of padded
 // tokens and non-local slots, which the grouping leaves out.
 struct GroupExactArgs {
@@ -1878,6 +1879,7 @@ __device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, in
 // a workgroup of several waves, whose lifetimes differ (channels that no pair
 // kept end at once), can start only when every SIMD of a CU has a free slot.
 constexpr int kGroupExactWaves = 1;
+constexpr int kExactChannels = 2;  // channels of one tile per grouped exact wave, in turn
 
 // The grouped exact launch's workgroups that are not (tile, channel) work:
 // the first kDownBuilders build the down order, those past the tile items run
@@ -1916,94 +1918,103 @@ __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, i
   return -1;
 }
 
-__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(8))) void
+__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(7))) void
 group_exact_kernel(GroupExactArgs a) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int lane = threadIdx.x & 63;
   const int block = group_exact_side_items(a, 64 * kGroupExactWaves);
   if (block < 0) return;
   const int z = block / a.channel_groups;
-  const int c = __builtin_amdgcn_readfirstlane((block % a.channel_groups) * kGroupExactWaves + wave);
-  if (c >= a.I) return;
-  // The tile count, the tile's expert, pair count and 16 pair slots and this
-  // channel's mask, through the scalar cache in one round trip: z < tile bound
-  // <= T * K keeps every address in bounds whatever the tile count, and only
-  // slots named by mask bits (< count) are used.
+  const int c0 = (block % a.channel_groups) * kExactChannels;
+  // The tile count, the tile's expert, pair count and 16 pair slots through
+  // the scalar cache, and lane l < 16 the mask of channel c0 + l, in one
+  // round trip: z < tile bound <= T * K keeps every address in bounds
+  // whatever the tile count, and only slots named by mask bits (< count) are
+  // used.
   const int total = load_uniform(a.group_total);
   const int e = load_uniform(a.group_experts + z);
   const int count = load_uniform(a.group_counts + z);
   const i32x16 slots = load_uniform(reinterpret_cast<const i32x16 *>(a.group_pairs + kGroupPairs * z));
-  const uint32_t mask_word = load_uniform(a.tile_masks + static_cast<long>(z) * a.I + c);
+  const int lane_channel = c0 + (lane & (kExactChannels - 1));
+  const bool lane_in = lane < kExactChannels && lane_channel < a.I;
+  const uint32_t mask_word =
+      lane_in ? load_global(a.tile_masks + static_cast<long>(z) * a.I + lane_channel) : 0u;
   // the neighbouring tiles' experts: an expert split into several tiles has
   // its rows read by each of them (entries past the count are never used)
   const int bound = a.tile_items / a.channel_groups;
   const int before = load_uniform(a.group_experts + max(z - 1, 0));
   const int after = load_uniform(a.group_experts + min(z + 1, bound - 1));
   // all issued before any is tested (else each waits under its branch)
-  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots), "s"(mask_word), "s"(before),
-               "s"(after));
+  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots), "s"(before), "s"(after));
   if (z >= total) return;
   const bool shared_rows = (z > 0 && before == e) || (z + 1 < total && after == e);
   // lane p < count: pair p of the tile
   int pair = slots[0];
 #pragma unroll
   for (int p = 1; p < kGroupPairs; ++p) pair = (lane & (kGroupPairs - 1)) == p ? slots[p] : pair;
-  const uint32_t mask = a.dense ? (1u << count) - 1u : mask_word;  // count <= 16
-  if (!mask) return;
-  const int token = pair / a.K, logical = (pair % a.K) * a.I + c;
-  // rows and hidden rows through buffer resources: lane offset 16 lane, part j
-  // at 1024 j bytes; parts past H read zeros and their chains are discarded
-  const int row_bytes = 2 * a.H, offset = 16 * lane;
-  const long grow = (static_cast<long>(e) * 2 * a.I + c) * a.H;
-  const __amdgpu_buffer_rsrc_t gate_rows = buffer_resource(a.gate_up + grow, row_bytes);
-  const __amdgpu_buffer_rsrc_t up_rows =
-      buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
-  constexpr int kParts = kHiddenParts;
-  uint4 xw[kParts];
-  auto load_hidden = [&](int pp) {
-    const int t = __builtin_amdgcn_readlane(token, pp);
-    const __amdgpu_buffer_rsrc_t hidden =
-        buffer_resource(a.x + static_cast<long>(t) * a.H, row_bytes);
+  const int token = pair / a.K, pair_slot = pair % a.K;
+  // count <= 16
+  const uint32_t lane_mask = a.dense ? (lane_in ? (1u << count) - 1u : 0u) : mask_word;
+  // the wave's channels that some pair kept, in order
+  for (uint64_t kept = __ballot(lane_mask != 0u); kept; kept &= kept - 1) {
+    const int at = __builtin_ctzll(kept);
+    const int c = c0 + at;
+    const uint32_t mask = __builtin_amdgcn_readlane(lane_mask, at);
+    const int logical = pair_slot * a.I + c;
+    // rows and hidden rows through buffer resources: lane offset 16 lane, part j
+    // at 1024 j bytes; parts past H read zeros and their chains are discarded
+    const int row_bytes = 2 * a.H, offset = 16 * lane;
+    const long grow = (static_cast<long>(e) * 2 * a.I + c) * a.H;
+    const __amdgpu_buffer_rsrc_t gate_rows = buffer_resource(a.gate_up + grow, row_bytes);
+    const __amdgpu_buffer_rsrc_t up_rows =
+        buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
+    constexpr int kParts = kHiddenParts;
+    uint4 xw[kParts];
+    auto load_hidden = [&](int pp) {
+      const int t = __builtin_amdgcn_readlane(token, pp);
+      const __amdgpu_buffer_rsrc_t hidden =
+          buffer_resource(a.x + static_cast<long>(t) * a.H, row_bytes);
 #pragma unroll
-    for (int j = 0; j < kParts; ++j) xw[j] = buffer_load16(hidden, offset + 1024 * j);
-  };
-  // the first keeping pair's hidden row travels with the gate/up rows
-  load_hidden(__builtin_ctz(mask));
-  // rows read once stream past the caches; rows the expert's other tiles read
-  // again stay cached for them
-  uint4 gw[kParts], uw[kParts];
-  if (shared_rows) {
+      for (int j = 0; j < kParts; ++j) xw[j] = buffer_load16(hidden, offset + 1024 * j);
+    };
+    // the first keeping pair's hidden row travels with the gate/up rows
+    load_hidden(__builtin_ctz(mask));
+    // rows read once stream past the caches; rows the expert's other tiles read
+    // again stay cached for them
+    uint4 gw[kParts], uw[kParts];
+    if (shared_rows) {
 #pragma unroll
-    for (int j = 0; j < kParts; ++j) {
-      gw[j] = buffer_load16(gate_rows, offset + 1024 * j);
-      uw[j] = buffer_load16(up_rows, offset + 1024 * j);
+      for (int j = 0; j < kParts; ++j) {
+        gw[j] = buffer_load16(gate_rows, offset + 1024 * j);
+        uw[j] = buffer_load16(up_rows, offset + 1024 * j);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kParts; ++j) {
+        gw[j] = buffer_stream16(gate_rows, offset + 1024 * j);
+        uw[j] = buffer_stream16(up_rows, offset + 1024 * j);
+      }
     }
-  } else {
+    // lane p holds pair p's sums; the results are stored after the loop (a
+    // store inside it would delay the next pair's loads, which wait in order)
+    float kept_g = 0.0f, kept_u = 0.0f;
+    for (uint32_t rest = mask; rest; rest &= rest - 1) {
+      const int pp = __builtin_ctz(rest);
+      if (rest != mask) load_hidden(pp);
+      float g = 0.0f, uu = 0.0f;
+      // keep the rows packed across pairs (unpacking them once ahead of the
+      // loop would hold 64 more registers and halve the waves per SIMD)
 #pragma unroll
-    for (int j = 0; j < kParts; ++j) {
-      gw[j] = buffer_stream16(gate_rows, offset + 1024 * j);
-      uw[j] = buffer_stream16(up_rows, offset + 1024 * j);
+      for (int j = 0; j < kParts; ++j)
+        asm volatile("" : "+v"(gw[j].x), "+v"(gw[j].y), "+v"(gw[j].z), "+v"(gw[j].w),
+                     "+v"(uw[j].x), "+v"(uw[j].y), "+v"(uw[j].z), "+v"(uw[j].w));
+      row_dots(gw, uw, xw, a.H, lane, g, uu);
+      g = wave_sum_lane0(g);
+      uu = wave_sum_lane0(uu);
+      kept_g = lane == pp ? g : kept_g;
+      kept_u = lane == pp ? uu : kept_u;
     }
+    if (lane < kGroupPairs && ((mask >> lane) & 1u)) exact_results(a, token, logical, kept_g, kept_u);
   }
-  // lane p holds pair p's sums; the results are stored after the loop (a
-  // store inside it would delay the next pair's loads, which wait in order)
-  float kept_g = 0.0f, kept_u = 0.0f;
-  for (uint32_t rest = mask; rest; rest &= rest - 1) {
-    const int pp = __builtin_ctz(rest);
-    if (rest != mask) load_hidden(pp);
-    float g = 0.0f, uu = 0.0f;
-    // keep the rows packed across pairs (unpacking them once ahead of the
-    // loop would hold 64 more registers and halve the waves per SIMD)
-#pragma unroll
-    for (int j = 0; j < kParts; ++j)
-      asm volatile("" : "+v"(gw[j].x), "+v"(gw[j].y), "+v"(gw[j].z), "+v"(gw[j].w),
-                   "+v"(uw[j].x), "+v"(uw[j].y), "+v"(uw[j].z), "+v"(uw[j].w));
-    row_dots(gw, uw, xw, a.H, lane, g, uu);
-    g = wave_sum_lane0(g);
-    uu = wave_sum_lane0(uu);
-    kept_g = lane == pp ? g : kept_g;
-    kept_u = lane == pp ? uu : kept_u;
-  }
-  if (lane < kGroupPairs && ((mask >> lane) & 1u)) exact_results(a, token, logical, kept_g, kept_u);
 }
 
 // ---------------------------------------------------------------------------
@@ -2812,7 +2823,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     gx.F = s.F;
     gx.T = tokens;
     gx.gelu = gelu;
-    gx.channel_groups = (s.I + kGroupExactWaves - 1) / kGroupExactWaves;
+    gx.channel_groups = (s.I + kExactChannels - 1) / kExactChannels;
     gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
     gx.encoder_t = en.encoder_t;
     gx.parts = en.parts;
