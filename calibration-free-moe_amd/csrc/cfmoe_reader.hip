@@ -1285,8 +1285,6 @@ struct SelectArgs {
   int32_t *starts;
   int32_t *tile_starts;
   int32_t *down_tile_starts;
-  double *read_work;  // slot 12 += union_row_bytes per (tile, channel) some pair kept (or NULL)
-  double union_row_bytes;
   int N, F, I, K;
   int thresholded;
 };
@@ -1377,7 +1375,6 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int wave_totals[kSelectWaves];
   __shared__ int slot_start[65];
   __shared__ int slot_tiles[64];
-  __shared__ int union_scratch[kSelectWaves];
   const int t = blockIdx.x, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
@@ -1385,15 +1382,40 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   if (tid < kSelectLastSlots) last[tid] = 0;
   const int per = (a.N + kSelectThreads - 1) / kSelectThreads;
   const int first = tid * per;
-  // keys: every load issued unconditionally (absent keys read a zero)
+  // keys: every load issued unconditionally (absent keys read a zero), four
+  // or two at a time when the thread's run allows (N is a multiple of 16, so
+  // a run of 4 or 2 keys is inside the row or wholly past it)
   uint32_t key[kKeys];
   const float *row = a.scores + static_cast<long>(t) * a.N;
+  auto normal = [](uint32_t bits) { return __float_as_uint(__uint_as_float(bits) + 0.0f); };
+  if (per % 4 == 0) {
 #pragma unroll
-  for (int j = 0; j < kKeys; ++j) {
-    const bool present = j < per && first + j < a.N;
-    const float *source =
-        present ? row + first + j : reinterpret_cast<const float *>(&kZeroVector);
-    key[j] = __float_as_uint(load_global(source) + 0.0f);
+    for (int j = 0; j < kKeys; j += 4) {
+      const bool present = j < per && first + j < a.N;
+      const uint4 v =
+          load_global(present ? reinterpret_cast<const uint4 *>(row + first + j) : &kZeroVector);
+      key[j] = normal(v.x);
+      key[j + 1] = normal(v.y);
+      key[j + 2] = normal(v.z);
+      key[j + 3] = normal(v.w);
+    }
+  } else if (per % 2 == 0) {
+#pragma unroll
+    for (int j = 0; j < kKeys; j += 2) {
+      const bool present = j < per && first + j < a.N;
+      const uint2 v = load_global(present ? reinterpret_cast<const uint2 *>(row + first + j)
+                                          : reinterpret_cast<const uint2 *>(&kZeroVector));
+      key[j] = normal(v.x);
+      key[j + 1] = normal(v.y);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kKeys; ++j) {
+      const bool present = j < per && first + j < a.N;
+      const float *source =
+          present ? row + first + j : reinterpret_cast<const float *>(&kZeroVector);
+      key[j] = normal(__float_as_uint(load_global(source)));
+    }
   }
   auto valid = [&](int j) { return j < per && first + j < a.N; };
   int want = a.F;
@@ -1469,7 +1491,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   }
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
   int above_before = packed & 0xffff, tied_before = packed >> 16;
-  int union_rows = 0;  // (tile, channel) words this thread turned nonzero
+  uint32_t kept_bits = 0;  // bit j: candidate first + j kept
   // the slot of the current candidate and the next slot start at or after
   // this thread's first candidate (no division per key)
   int slot = first / a.I, next_slot = (first + a.I - 1) / a.I, boundary = next_slot * a.I;
@@ -1490,8 +1512,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
       keep = tied_before < room;
       ++tied_before;
     }
-    a.selected[static_cast<long>(t) * a.N + i] = keep;
-    a.completed[static_cast<long>(t) * a.N + i] = 0;
+    kept_bits |= static_cast<uint32_t>(keep) << j;
     const int position = above_before + min(tied_before - (keep && key[j] == cutoff ? 1 : 0), room);
     if (keep) {
       if (key[j] > cutoff) ++above_before;
@@ -1499,31 +1520,46 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
         a.next_ids[static_cast<long>(t) * a.F + position] = i;
         // the channel's bit for this pair in its tile's mask (OR: any order)
         const int slot_tile = a.tile_masks ? slot_tiles[slot] : -1;
-        if (slot_tile >= 0) {
-          const uint32_t before = atomicOr(
-              &a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
-              1u << (slot_tile % kGroupPairs));
-          union_rows += before == 0u;  // the first pair of its tile to keep the channel
-        }
+        if (slot_tile >= 0)
+          atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
+                   1u << (slot_tile % kGroupPairs));
       }
+    }
+  }
+  // the run's selected flags (and cleared completed flags) as one store per
+  // 4 or 2 candidates where the run allows
+  {
+    uint8_t *selected = a.selected + static_cast<long>(t) * a.N + first;
+    uint8_t *completed = a.completed + static_cast<long>(t) * a.N + first;
+    auto flag = [&](int j) { return (kept_bits >> j) & 1u; };
+    if (per % 4 == 0) {
+#pragma unroll
+      for (int j = 0; j < kKeys; j += 4)
+        if (j < per && first + j < a.N) {
+          *reinterpret_cast<uint32_t *>(selected + j) =
+              flag(j) | flag(j + 1) << 8 | flag(j + 2) << 16 | flag(j + 3) << 24;
+          *reinterpret_cast<uint32_t *>(completed + j) = 0u;
+        }
+    } else if (per % 2 == 0) {
+#pragma unroll
+      for (int j = 0; j < kKeys; j += 2)
+        if (j < per && first + j < a.N) {
+          *reinterpret_cast<uint16_t *>(selected + j) = static_cast<uint16_t>(flag(j) | flag(j + 1) << 8);
+          *reinterpret_cast<uint16_t *>(completed + j) = 0;
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kKeys; ++j)
+        if (j < per && first + j < a.N) {
+          selected[j] = static_cast<uint8_t>(flag(j));
+          completed[j] = 0;
+        }
     }
   }
   for (int p = kept_total + tid; p < a.F; p += kSelectThreads)
     a.next_ids[static_cast<long>(t) * a.F + p] = -1;
   if (tid == 0) slot_start[a.K] = min(kept_total, a.F);
-  // each union row of the grouped exact rows is counted once, by the token
-  // whose select turned its word nonzero: per-wave sums meet at the barrier
-  // below, wave 0 adds them (one FP64 add per token)
-  if (a.read_work) {
-    const int rows = wave_sum_all(union_rows);
-    if ((tid & 63) == 0) union_scratch[tid >> 6] = rows;
-  }
   __syncthreads();
-  if (a.read_work && tid == 0) {
-    int rows = 0;
-    for (int w = 0; w < kSelectWaves; ++w) rows += union_scratch[w];
-    if (rows > 0) atomicAdd(a.read_work + 12, rows * a.union_row_bytes);
-  }
   // wave 0: lane k writes slot k's count, start and tile starts (K <= 64)
   if (tid < kWave) {
     const bool slot = tid < a.K;
@@ -1746,10 +1782,15 @@ struct GroupExactArgs {
   const int32_t *pair_tiles;
   const int32_t *down_tile_starts;
   int max_tiles, down_blocks, order_words, slot_capacity;
+  // union-row accounting (or NULL): kUnionCounters workgroups after the
+  // builders add union_row_bytes to slot 12 per nonzero tile mask word
+  double *read_work;
+  double union_row_bytes;
 };
 
 constexpr int kMaxHidden = 2048;
-constexpr int kDownBuilders = 8;  // one per XCD
+constexpr int kDownBuilders = 8;     // one per XCD
+constexpr int kUnionCounters = 64;  // workgroups counting the tile masks' nonzero words
 constexpr int kHiddenParts = kMaxHidden / 512;  // 16-byte parts per lane of a hidden-size row
 
 // Lane-ordered gate and up dots with a hidden row, each row held as
@@ -1865,6 +1906,28 @@ __device__ void build_down_order(const GroupExactArgs &a, int x) {
   for (int r = max(hi - lo, 0) + lane; r < a.down_blocks / 8; r += kWave) a.down_order[8 * r + x] = -1;
 }
 
+// Counter x of the union rows: the nonzero (tile, channel) mask words of
+// the routing's tiles, four loads per lane in flight, one FP64 add per
+// workgroup. Each word is counted once, whichever pairs set it.
+__device__ void count_union_rows(const GroupExactArgs &a, int x) {
+  const int lane = threadIdx.x & 63;
+  const long words = static_cast<long>(load_global(a.group_total)) * a.I;
+  int rows = 0;
+  for (long w0 = static_cast<long>(x) * 4 * kWave; w0 < words;
+       w0 += static_cast<long>(kUnionCounters) * 4 * kWave) {
+    uint32_t m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long w = w0 + u * kWave + lane;
+      m[u] = load_global(a.tile_masks + min(w, words - 1));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rows += w0 + u * kWave + lane < words && m[u] != 0u;
+  }
+  rows = wave_sum_all(rows);
+  if (lane == 0 && rows > 0) atomicAdd(a.read_work + 12, rows * a.union_row_bytes);
+}
+
 __device__ __forceinline__ void exact_results(const GroupExactArgs &a, int t, int logical,
                                               float g, float u) {
   const long address = static_cast<long>(t) * 2 * a.N + logical;
@@ -1894,6 +1957,13 @@ __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, i
       return -1;
     }
     block -= kDownBuilders;
+  }
+  if (a.read_work) {
+    if (block < kUnionCounters) {
+      count_union_rows(a, block);
+      return -1;
+    }
+    block -= kUnionCounters;
   }
   if (block < a.tile_items) return block;
   const int item = block - a.tile_items;
@@ -2657,15 +2727,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   sel.I = s.I;
   sel.K = s.K;
   sel.thresholded = (flags & CFMOE_THRESHOLD) != 0;
-  // per-(tile, channel) pair masks for the grouped exact kernel; the select
-  // kernel counts their nonzero words as the union rows the grouped exact
-  // launch reads (4 H bytes each)
+  // per-(tile, channel) pair masks for the grouped exact kernel; that launch
+  // counts their nonzero words as the union rows it reads (4 H bytes each)
   const bool grouped = tokens >= s.grouped_tokens;
   const bool masked = s.screened && grouped;
   sel.pair_tiles = workspace->pair_tiles;
   sel.tile_masks = masked ? workspace->tile_masks : nullptr;
-  sel.read_work = masked && (flags & CFMOE_ACCOUNT) ? workspace->read_work : nullptr;
-  sel.union_row_bytes = 4.0 * s.H;
 
   if (s.screened) {
     const uint2 *trit_planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
@@ -2836,8 +2903,11 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     gx.down_blocks = down_blocks;
     gx.order_words = static_cast<int>(down_list_words(workspace->capacity, s));
     gx.slot_capacity = static_cast<int>(down_slot_capacity(workspace->capacity, s));
+    gx.read_work = masked && (flags & CFMOE_ACCOUNT) ? workspace->read_work : nullptr;
+    gx.union_row_bytes = 4.0 * s.H;
+    const int counters = gx.read_work ? kUnionCounters : 0;
     hipLaunchKernelGGL(group_exact_kernel,
-                       dim3(kDownBuilders + gx.tile_items + gx.encode_items + tokens),
+                       dim3(kDownBuilders + counters + gx.tile_items + gx.encode_items + tokens),
                        dim3(64 * kGroupExactWaves), 0, stream, gx);
     if ((rc = check_launch("exact"))) return rc;
   } else if (stages & (1u << CFMOE_STAGE_EXACT)) {
