@@ -779,10 +779,48 @@ __device__ void score_absent_slots(const Args &a, int t, int threads) {
 // Score of four channels for one pair from the gate and up estimates (and
 // variances); writes the projections, variances and scores
 // (progressive.py:1265-1353).
+// The score's inputs for one pair and four channels, loaded ahead of the
+// screen's arithmetic (so the epilogue waits on no load of its own).
+struct ScoreInputs {
+  float weight;
+  float norm[4], alpha[4], beta[4];
+};
+
+template <class Args>
+__device__ __forceinline__ ScoreInputs load_score_inputs(const Args &a, int e, int token, int slot,
+                                                         int c) {
+  ScoreInputs in;
+  in.weight = a.weights[token * a.K + slot];
+  const float4 norm = *reinterpret_cast<const float4 *>(a.norms + static_cast<long>(e) * a.I + c);
+  in.norm[0] = norm.x;
+  in.norm[1] = norm.y;
+  in.norm[2] = norm.z;
+  in.norm[3] = norm.w;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    in.alpha[r] = 0.0f;
+    in.beta[r] = 0.0f;
+  }
+  if (a.geometry) {
+    const float4 g01 = *reinterpret_cast<const float4 *>(a.geometry + (static_cast<long>(e) * a.I + c) * 2);
+    const float4 g23 = *reinterpret_cast<const float4 *>(a.geometry + (static_cast<long>(e) * a.I + c) * 2 + 4);
+    in.alpha[0] = g01.x;
+    in.beta[0] = g01.y;
+    in.alpha[1] = g01.z;
+    in.beta[1] = g01.w;
+    in.alpha[2] = g23.x;
+    in.beta[2] = g23.y;
+    in.alpha[3] = g23.z;
+    in.beta[3] = g23.w;
+  }
+  return in;
+}
+
 template <bool kGh5, class Args>
 __device__ __forceinline__ void score_four(const Args &a, int e, int token, int slot, int c,
                                            const float gate[4], const float up[4],
-                                           const float gate_var[4], const float up_var[4]) {
+                                           const float gate_var[4], const float up_var[4],
+                                           const ScoreInputs &in) {
   const long base = static_cast<long>(token) * 2 * a.N + static_cast<long>(slot) * a.I + c;
   *reinterpret_cast<float4 *>(a.partial + base) = make_float4(gate[0], gate[1], gate[2], gate[3]);
   *reinterpret_cast<float4 *>(a.partial + base + a.N) = make_float4(up[0], up[1], up[2], up[3]);
@@ -792,20 +830,11 @@ __device__ __forceinline__ void score_four(const Args &a, int e, int token, int 
     *reinterpret_cast<float4 *>(a.variances + base + a.N) =
         make_float4(up_var[0], up_var[1], up_var[2], up_var[3]);
   }
-  const float weight = a.weights[token * a.K + slot];
-  const float4 norm = *reinterpret_cast<const float4 *>(a.norms + static_cast<long>(e) * a.I + c);
-  const float norms4[4] = {norm.x, norm.y, norm.z, norm.w};
   float score[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float alpha = 0.0f, beta = 0.0f;
-    if (a.geometry) {
-      alpha = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2];
-      beta = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2 + 1];
-    }
-    score[r] = cfm_score(gate[r], up[r], gate_var[r], up_var[r], norms4[r], weight, alpha, beta,
-                         a.gelu != 0, a.point != 0);
-  }
+  for (int r = 0; r < 4; ++r)
+    score[r] = cfm_score(gate[r], up[r], gate_var[r], up_var[r], in.norm[r], in.weight, in.alpha[r],
+                         in.beta[r], a.gelu != 0, a.point != 0);
   *reinterpret_cast<float4 *>(a.scores + static_cast<long>(token) * a.N + static_cast<long>(slot) * a.I + c) =
       make_float4(score[0], score[1], score[2], score[3]);
 }
@@ -914,6 +943,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   __syncthreads();
   const bool live_pair = pp < count;
   const long pair_cell = static_cast<long>(pair_token[min(pp, count - 1)]) * B;
+  // the score's inputs (used by wave 0's live lanes) in this round trip
+  const ScoreInputs inputs = load_score_inputs(a, e, pair_token[min(pp, count - 1)],
+                                               pair_slot[min(pp, count - 1)],
+                                               kRowTile * ct + row_in_tile);
   // the lane's pair's grid sums, exponents (and kept norms) of the wave's blocks
   int qsum[kWaveSplits][kMaxSpan], shift[kWaveSplits][kMaxSpan];
   float n2[kWaveSplits][kMaxSpan];
@@ -1018,7 +1051,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
         if (kGh5) var[up][r] = var[up][r] + vparts[s][up][lane][r];
       }
   score_four<kGh5>(a, e, pair_token[pp], pair_slot[pp], kRowTile * ct + row_in_tile, est[0], est[1],
-                   var[0], var[1]);
+                   var[0], var[1], inputs);
 }
 
 
@@ -1239,33 +1272,11 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
   if (a.tile_masks && lane < kRowTile)
     a.tile_masks[static_cast<long>(z) * a.I + kRowTile * ct + lane] = 0u;
   if (pp >= count) return;
-  const int token = sh.pair_token[pp], slot = sh.pair_slot[pp];
+  // (the score's inputs here: held across the splits they would cost a wave per SIMD)
   const int c = kRowTile * ct + row_in_tile;
-  const long base = static_cast<long>(token) * 2 * a.N + static_cast<long>(slot) * a.I + c;
-  *reinterpret_cast<float4 *>(a.partial + base) = make_float4(est[0][0], est[0][1], est[0][2], est[0][3]);
-  *reinterpret_cast<float4 *>(a.partial + base + a.N) =
-      make_float4(est[1][0], est[1][1], est[1][2], est[1][3]);
-  if (kGh5) {
-    *reinterpret_cast<float4 *>(a.variances + base) = make_float4(var[0][0], var[0][1], var[0][2], var[0][3]);
-    *reinterpret_cast<float4 *>(a.variances + base + a.N) =
-        make_float4(var[1][0], var[1][1], var[1][2], var[1][3]);
-  }
-  const float weight = a.weights[token * a.K + slot];
-  const float4 norm = *reinterpret_cast<const float4 *>(a.norms + static_cast<long>(e) * a.I + c);
-  const float norms4[4] = {norm.x, norm.y, norm.z, norm.w};
-  float score[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    float alpha = 0.0f, beta = 0.0f;
-    if (a.geometry) {
-      alpha = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2];
-      beta = a.geometry[(static_cast<long>(e) * a.I + c + r) * 2 + 1];
-    }
-    score[r] = cfm_score(est[0][r], est[1][r], var[0][r], var[1][r], norms4[r], weight, alpha,
-                         beta, a.gelu != 0, a.point != 0);
-  }
-  *reinterpret_cast<float4 *>(a.scores + static_cast<long>(token) * a.N + static_cast<long>(slot) * a.I + c) =
-      make_float4(score[0], score[1], score[2], score[3]);
+  const ScoreInputs inputs = load_score_inputs(a, e, sh.pair_token[pp], sh.pair_slot[pp], c);
+  score_four<kGh5>(a, e, sh.pair_token[pp], sh.pair_slot[pp], c, est[0], est[1], var[0], var[1],
+                   inputs);
 }
 
 // ---------------------------------------------------------------------------
@@ -2697,8 +2708,11 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
                       reinterpret_cast<uintptr_t>(workspace->variances) |
                       reinterpret_cast<uintptr_t>(workspace->scores) |
                       reinterpret_cast<uintptr_t>(workspace->digits) |
-                      reinterpret_cast<uintptr_t>(weights->norms)) % 16))
-    return fail(CFMOE_EINVAL, "partial, variances, scores, digits and norms must be 16-byte aligned");
+                      reinterpret_cast<uintptr_t>(weights->norms) |
+                      reinterpret_cast<uintptr_t>((dims->flags & CFMOE_GEOMETRY) ? weights->geometry
+                                                                           : nullptr)) % 16))
+    return fail(CFMOE_EINVAL,
+                "partial, variances, scores, digits, norms and geometry must be 16-byte aligned");
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
   const uint32_t flags = dims->flags;
   const bool gh5 = !(flags & CFMOE_POINT);
