@@ -163,6 +163,26 @@ __device__ __forceinline__ uint2 load_global(const uint2 *p) {
   return make_uint2(v.x, v.y);
 }
 
+// Loads at a 32-bit byte offset from a wave-uniform base: the address stays
+// base (scalar registers) + offset (one vector register) instead of a 64-bit
+// vector address per lane.
+template <typename V>
+__device__ __forceinline__ V load_vector_at(const void *base, uint32_t offset) {
+  const __attribute__((address_space(1))) char *b =
+      reinterpret_cast<const __attribute__((address_space(1))) char *>(reinterpret_cast<uintptr_t>(base));
+  return *reinterpret_cast<const __attribute__((address_space(1))) V *>(b + offset);
+}
+
+__device__ __forceinline__ uint2 load_uint2_at(const void *base, uint32_t offset) {
+  const u32x2 v = load_vector_at<u32x2>(base, offset);
+  return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ uint4 load_uint4_at(const void *base, uint32_t offset) {
+  const u32x4 v = load_vector_at<u32x4>(base, offset);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Load source of dead lanes (no branch around a load, no select after it).
 __device__ const uint4 kZeroVector = {0, 0, 0, 0};
 
@@ -739,13 +759,32 @@ __device__ __forceinline__ v4i expand_digits(uint32_t x) {
              static_cast<int>((x >> 4) & 0x03030303u), static_cast<int>((x >> 6) & 0x03030303u)};
 }
 
-// acc0 + 2^8 acc1 + 2^16 acc2 as two shift-adds (v_lshl_add_u32; the empty
-// asm keeps the compiler from re-forming two shifts and a three-way add). The
-// partial sums wrap like the full one, which is below 2^31 in magnitude.
-__device__ __forceinline__ int combine_digits(int acc0, int acc1, int acc2) {
-  uint32_t high = (static_cast<uint32_t>(acc2) << 8) + static_cast<uint32_t>(acc1);
-  asm volatile("" : "+v"(high));
-  return static_cast<int>((high << 8) + static_cast<uint32_t>(acc0));
+// The gate (up = 0) and up (up = 1) row tiles' integer dots with a pair's
+// grid values q = d0 + 2^8 d1 + 2^16 d2 over one 128-coordinate block, minus
+// the block's grid sum (`start`): the trits a come as digits 0..2 (a0 and a1:
+// coordinates 0-63 and 64-127), so sum (a - 1) q = sum a q - sum q. The digit
+// planes go through one accumulator per row tile, high digit first, the
+// running sum shifted left by 8 before each lower digit: ((s2 2^8) + s1) 2^8
+// + s0 - qsum, the integer sum_a (d0 + 2^8 d1 + 2^16 d2) - qsum exactly (every
+// step is a 32-bit integer add or shift; the top digit is below 2^5 in
+// magnitude, so no step leaves the int32 range). operand(h, d) is the B
+// operand of coordinate half h and digit d.
+template <typename Operand>
+__device__ __forceinline__ void digit_dots(const v4i (&a0)[2], const v4i (&a1)[2], v4i start,
+                                           Operand operand, v4i (&acc)[2]) {
+  const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+  for (int d = 2; d >= 0; --d) {
+    const v4i b0 = operand(0, d);
+#pragma unroll
+    for (int up = 0; up < 2; ++up) {
+      const v4i c = d == 2 ? zero : (d == 0 ? (acc[up] << 8) + start : acc[up] << 8);
+      acc[up] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[up], b0, c, 0, 0, 0);
+    }
+    const v4i b1 = operand(1, d);
+#pragma unroll
+    for (int up = 0; up < 2; ++up) acc[up] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[up], b1, acc[up], 0, 0, 0);
+  }
 }
 
 __device__ __forceinline__ float half_at(uint32_t word, int high) {
@@ -885,6 +924,12 @@ struct StepLoads {
   uint2 words, scale, residual;
 };
 
+// An empty use of a step's registers: the wait for its loads happens here,
+// on every path, and not where the compiler would merge paths (a loop head).
+__device__ __forceinline__ void consume(const StepLoads &l) {
+  asm volatile("" ::"v"(l.words.x), "v"(l.words.y), "v"(l.scale.x), "v"(l.scale.y));
+}
+
 constexpr int kWaveSplits = (kMaxSplits + kSmallWaves - 1) / kSmallWaves;
 constexpr int kWaveBlocks = kWaveSplits * kMaxSpan;
 
@@ -993,27 +1038,13 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
         a0[up] = expand_digits(step[si][j][up].words.x);
         a1[up] = expand_digits(step[si][j][up].words.y);
       }
-      v4i acc[2][3];
-#pragma unroll
-      for (int d = 0; d < 3; ++d) {
-        const v4i b0 = operand(0, d);
-#pragma unroll
-        for (int up = 0; up < 2; ++up)
-          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[up], b0, d == 0 ? start : v4i{0, 0, 0, 0},
-                                                            0, 0, 0);
-      }
-#pragma unroll
-      for (int d = 0; d < 3; ++d) {
-        const v4i b1 = operand(1, d);
-#pragma unroll
-        for (int up = 0; up < 2; ++up)
-          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[up], b1, acc[up][d], 0, 0, 0);
-      }
+      v4i acc[2];
+      digit_dots(a0, a1, start, operand, acc);
 #pragma unroll
       for (int up = 0; up < 2; ++up)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int sum = combine_digits(acc[up][0][r], acc[up][1][r], acc[up][2][r]);
+          const int sum = acc[up][r];
           const float dot = ldexpf(static_cast<float>(sum), -shift[si][j]);
           const uint32_t sw = r < 2 ? step[si][j][up].scale.x : step[si][j][up].scale.y;
           part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);
@@ -1107,7 +1138,7 @@ struct FusedShared {
 };
 
 template <bool kGh5>
-__global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreenArgs a) {
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kGh5 ? 3 : 4))) void fused_screen_kernel(FusedScreenArgs a) {
   __shared__ FusedShared sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int B = a.H / 128;
@@ -1127,24 +1158,27 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
   const int pp = lane % 16, k0 = 16 * (lane / 16), row_in_tile = 4 * (lane / 16);
   const int span = a.span, splits = a.splits;
   // the wave's planes and scales: gate row tile cc, up row tile CT + cc
-  const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64 + lane;
-  const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I + row_in_tile;
+  // (byte offsets from the expert's planes and scales)
+  const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64;
+  const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I;
   auto load_step = [&](int s, int bl, int up) {
     StepLoads l;
     const int b = min(s * span + min(bl, span - 1), B - 1);  // past H: a repeat, unused
     const int rt = up ? CT + cc : cc;
-    l.words = load_global(planes + (static_cast<long>(b) * RT + rt) * 64);
-    const uint16_t *plane = stats + static_cast<long>(b) * 4 * a.I + kRowTile * rt;
-    l.scale = load_global(reinterpret_cast<const uint2 *>(plane));
-    if (kGh5) l.residual = load_global(reinterpret_cast<const uint2 *>(plane + 2 * a.I));
+    l.words = load_uint2_at(planes, static_cast<uint32_t>(((b * RT + rt) * 64 + lane) * 8));
+    const uint32_t plane = static_cast<uint32_t>((b * 4 * a.I + kRowTile * rt + row_in_tile) * 2);
+    l.scale = load_uint2_at(stats, plane);
+    if (kGh5) l.residual = load_uint2_at(stats, plane + 4 * a.I);
     return l;
   };
-  // split 0's steps in flight while the tile is staged
-  StepLoads step[kMaxSpan][2];
+  // split 0's steps in flight while the tile is staged; step[s % 2] holds
+  // split s's (the split loop runs two at a time, so the ring index is static
+  // and no register copy at a split's end waits for the next split's loads)
+  StepLoads step[2][kMaxSpan][2];
 #pragma unroll
   for (int bl = 0; bl < kMaxSpan; ++bl)
 #pragma unroll
-    for (int up = 0; up < 2; ++up) step[bl][up] = load_step(0, bl, up);
+    for (int up = 0; up < 2; ++up) step[0][bl][up] = load_step(0, bl, up);
 
   // ---- the tile's pairs and per-(block, pair) constants
   if (tid < kPairTile) {
@@ -1174,8 +1208,8 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
       const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
       const int b = s * span + bl;
       const bool live = s < splits && item < kStageItems && p < count && bl < span && b < B;
-      const long cell = static_cast<long>(sh.pair_token[live ? p : 0]) * B + (live ? b : 0);
-      held[j] = live ? load_global(reinterpret_cast<const uint4 *>(a.digits + (cell * 3 + d) * 128) + piece)
+      const int cell = sh.pair_token[live ? p : 0] * B + (live ? b : 0);
+      held[j] = live ? load_uint4_at(a.digits, static_cast<uint32_t>((cell * 3 + d) * 128 + 16 * piece))
                      : make_uint4(0u, 0u, 0u, 0u);
     }
   };
@@ -1198,11 +1232,28 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
   __syncthreads();
 
   float est[2][4] = {}, var[2][4] = {};
-  for (int s = 0; s < splits; ++s) {
+  for (int s0 = 0; s0 < splits; s0 += 2)
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int s = s0 + h;
+    if (s >= splits) {
+      // (an odd split count: the last split's successor loads are read here,
+      // so no path round the loop leaves them in flight)
+#pragma unroll
+      for (int bl = 0; bl < kMaxSpan; ++bl)
+#pragma unroll
+        for (int up = 0; up < 2; ++up) consume(step[1][bl][up]);
+      break;
+    }
     const int buffer = s % kStageBuffers;
     // split s + kStageAhead's digits go to the buffer split s - 1 used, which
     // every wave finished before the last barrier
     stage_load(s + kStageAhead, held);
+    // split s + 1's steps (a repeat of split s's past the last)
+#pragma unroll
+    for (int bl = 0; bl < kMaxSpan; ++bl)
+#pragma unroll
+      for (int up = 0; up < 2; ++up) step[h ^ 1][bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);
     float part[2][4] = {}, vpart[2][4] = {};
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
@@ -1215,37 +1266,21 @@ __global__ __launch_bounds__(kFusedThreads) void fused_screen_kernel(FusedScreen
         return *reinterpret_cast<const v4i *>(&sh.digits[buffer][bl][d][pp][64 * h + k0]);
       };
       // gate and up row tiles share each B operand read
-      StepLoads l[2];
+      const StepLoads *l = step[h][bl];
       v4i a0[2], a1[2];
 #pragma unroll
       for (int up = 0; up < 2; ++up) {
-        l[up] = step[bl][up];
-        step[bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);  // its successor
         a0[up] = expand_digits(l[up].words.x);
         a1[up] = expand_digits(l[up].words.y);
       }
       if (!live_block) continue;
-      v4i acc[2][3];
-#pragma unroll
-      for (int d = 0; d < 3; ++d) {
-        const v4i b0 = operand(0, d);
-#pragma unroll
-        for (int up = 0; up < 2; ++up)
-          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[up], b0, d == 0 ? start : v4i{0, 0, 0, 0},
-                                                            0, 0, 0);
-      }
-#pragma unroll
-      for (int d = 0; d < 3; ++d) {
-        const v4i b1 = operand(1, d);
-#pragma unroll
-        for (int up = 0; up < 2; ++up)
-          acc[up][d] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1[up], b1, acc[up][d], 0, 0, 0);
-      }
+      v4i acc[2];
+      digit_dots(a0, a1, start, operand, acc);
 #pragma unroll
       for (int up = 0; up < 2; ++up)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int sum = combine_digits(acc[up][0][r], acc[up][1][r], acc[up][2][r]);
+          const int sum = acc[up][r];
           const float dot = ldexpf(static_cast<float>(sum), -shift);
           const uint32_t sw = r < 2 ? l[up].scale.x : l[up].scale.y;
           part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);
