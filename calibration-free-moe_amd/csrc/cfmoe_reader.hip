@@ -156,6 +156,7 @@ __device__ __forceinline__ uint4 load_global(const uint4 *p) {
 }
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ uint2 load_global(const uint2 *p) {
   const u32x2 v = *reinterpret_cast<const __attribute__((address_space(1))) u32x2 *>(
@@ -770,15 +771,24 @@ __device__ __forceinline__ v4i expand_digits(uint32_t x) {
 // magnitude, so no step leaves the int32 range). operand(h, d) is the B
 // operand of coordinate half h and digit d.
 template <typename Operand>
-__device__ __forceinline__ void digit_dots(const v4i (&a0)[2], const v4i (&a1)[2], v4i start,
+__device__ __forceinline__ void digit_dots(const v4i (&a0)[2], const v4i (&a1)[2], int start,
                                            Operand operand, v4i (&acc)[2]) {
   const v4i zero = {0, 0, 0, 0};
+  // an opaque start: (x << 8) + start is then one v_lshl_add_u32 (a known
+  // negation would become a shift and a subtract). The empty asm emits no
+  // instruction; an instruction in inline asm reading an MFMA result would
+  // get none of the compiler's wait states for that read.
+  asm volatile("" : "+v"(start));
 #pragma unroll
   for (int d = 2; d >= 0; --d) {
     const v4i b0 = operand(0, d);
 #pragma unroll
     for (int up = 0; up < 2; ++up) {
-      const v4i c = d == 2 ? zero : (d == 0 ? (acc[up] << 8) + start : acc[up] << 8);
+      v4i c = zero;
+      if (d == 1) c = acc[up] << 8;
+      if (d == 0)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) c[r] = (acc[up][r] << 8) + start;
       acc[up] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0[up], b0, c, 0, 0, 0);
     }
     const v4i b1 = operand(1, d);
@@ -930,6 +940,7 @@ __device__ __forceinline__ void consume(const StepLoads &l) {
   asm volatile("" ::"v"(l.words.x), "v"(l.words.y), "v"(l.scale.x), "v"(l.scale.y));
 }
 
+
 constexpr int kWaveSplits = (kMaxSplits + kSmallWaves - 1) / kSmallWaves;
 constexpr int kWaveBlocks = kWaveSplits * kMaxSpan;
 
@@ -1026,7 +1037,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
       const int b = s * span + j;
       if (j >= span || b >= B) break;
       const int bl = b - b_begin;
-      const v4i start = v4i{-qsum[si][j], -qsum[si][j], -qsum[si][j], -qsum[si][j]};
+      const int start = -qsum[si][j];
       auto operand = [&](int h, int d) {
         const v4i v = *reinterpret_cast<const v4i *>(
             mine + ((bl * 3 + d) * a.max_pairs + my_row) * kDigitStride + 64 * h + k0);
@@ -1129,17 +1140,22 @@ struct FusedScreenArgs {
   int gelu, point;
 };
 
+template <bool kGh5>
 struct FusedShared {
   alignas(16) int8_t digits[kStageBuffers][kMaxSpan][3][kPairTile][kDigitStride];
+  // the split's FP16 scales (and residual scales) of the workgroup's four
+  // gate and four up row tiles: entry 64 kind + 32 bl + 16 up + 4 w + q holds
+  // rows 4q .. 4q + 3 of wave w's row tile
+  uint2 scales[kStageBuffers][kGh5 ? 128 : 64];
   int qsum[16][kPairTile];  // blocks (H <= 2048) x pairs
   int shift[16][kPairTile];
-  float norm2[16][kPairTile];
+  float norm2[kGh5 ? 16 : 1][kPairTile];
   int pair_token[kPairTile], pair_slot[kPairTile];
 };
 
 template <bool kGh5>
-__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kGh5 ? 3 : 4))) void fused_screen_kernel(FusedScreenArgs a) {
-  __shared__ FusedShared sh;
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kGh5 ? 3 : 5))) void fused_screen_kernel(FusedScreenArgs a) {
+  __shared__ FusedShared<kGh5> sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int B = a.H / 128;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
@@ -1150,35 +1166,31 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   const int z = blockIdx.x / a.channel_groups;
   if (z >= load_uniform(a.group_total)) return;
   const int CT = a.I / kRowTile, RT = 2 * CT;
-  const int ct = (blockIdx.x % a.channel_groups) * kFusedWaves + wave;
+  const int group = blockIdx.x % a.channel_groups;
+  const int ct = group * kFusedWaves + wave;
   const bool working = ct < CT;  // a wave past the channels still stages and waits
   const int cc = min(ct, CT - 1);
   const int e = load_uniform(a.group_experts + z);
   const int count = load_uniform(a.group_counts + z);
   const int pp = lane % 16, k0 = 16 * (lane / 16), row_in_tile = 4 * (lane / 16);
   const int span = a.span, splits = a.splits;
-  // the wave's planes and scales: gate row tile cc, up row tile CT + cc
-  // (byte offsets from the expert's planes and scales)
+  // the wave's trit planes: gate row tile cc, up row tile CT + cc (byte
+  // offsets from the expert's planes); the scales come with the staging
   const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64;
   const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I;
   auto load_step = [&](int s, int bl, int up) {
-    StepLoads l;
     const int b = min(s * span + min(bl, span - 1), B - 1);  // past H: a repeat, unused
     const int rt = up ? CT + cc : cc;
-    l.words = load_uint2_at(planes, static_cast<uint32_t>(((b * RT + rt) * 64 + lane) * 8));
-    const uint32_t plane = static_cast<uint32_t>((b * 4 * a.I + kRowTile * rt + row_in_tile) * 2);
-    l.scale = load_uint2_at(stats, plane);
-    if (kGh5) l.residual = load_uint2_at(stats, plane + 4 * a.I);
-    return l;
+    return load_uint2_at(planes, static_cast<uint32_t>(((b * RT + rt) * 64 + lane) * 8));
   };
-  // split 0's steps in flight while the tile is staged; step[s % 2] holds
-  // split s's (the split loop runs two at a time, so the ring index is static
-  // and no register copy at a split's end waits for the next split's loads)
-  StepLoads step[2][kMaxSpan][2];
+  // split 0's steps in flight while the tile is staged; each step's
+  // successor (the next split's) is loaded into its registers as soon as the
+  // step is expanded
+  uint2 step[kMaxSpan][2];
 #pragma unroll
   for (int bl = 0; bl < kMaxSpan; ++bl)
 #pragma unroll
-    for (int up = 0; up < 2; ++up) step[0][bl][up] = load_step(0, bl, up);
+    for (int up = 0; up < 2; ++up) step[bl][up] = load_step(0, bl, up);
 
   // ---- the tile's pairs and per-(block, pair) constants
   if (tid < kPairTile) {
@@ -1193,102 +1205,104 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     const long cell = live ? static_cast<long>(sh.pair_token[p]) * B + b : 0;
     sh.qsum[b][p] = live ? a.qsums[cell] : 0;
     sh.shift[b][p] = live ? a.qexp[cell] : 0;
-    sh.norm2[b][p] = live && kGh5 ? a.norm2[cell] : 0.0f;
+    if (kGh5) sh.norm2[kGh5 ? b : 0][p] = live ? a.norm2[cell] : 0.0f;
   }
   // staging of split s: rows (block, digit, pair) of 128 bytes, 16 bytes per
-  // thread and item; pairs past the count and blocks past H are zero
+  // thread and item. Every load is unconditional and in bounds: a pair past
+  // the count reads the tile's first pair (its MFMA B column feeds only that
+  // pair's unused results) and a block past H or the split reads block B - 1
+  // (never used)
   constexpr int kStageRows = kMaxSpan * 3 * kPairTile;
   constexpr int kStageItems = kStageRows * 8;  // uint4 per split
-  constexpr int kStagePerThread = (kStageItems + kFusedThreads - 1) / kFusedThreads;
-  auto stage_load = [&](int s, uint4 *held) {
+  constexpr int kStagePerThread = kStageItems / kFusedThreads;
+  static_assert(kStageItems % kFusedThreads == 0, "staging items per thread");
+  // Thread i also loads scale entry i (see FusedShared; threads past the
+  // entries repeat entry i % entries, and a row tile past the channels reads
+  // the last one)
+  constexpr int kScaleEntries = kGh5 ? 128 : 64;
+  const int sk = kGh5 ? (tid >> 6) & 1 : 0, sbl = (tid >> 5) & 1, sup = (tid >> 4) & 1;
+  const int stile = (sup ? CT : 0) + min(group * kFusedWaves + ((tid >> 2) & 3), CT - 1);
+  const int srow = (sk ? 2 * a.I : 0) + kRowTile * stile + 4 * (tid & 3);
+  auto stage_load = [&](int s, uint4 *held, uint2 &scale) {
 #pragma unroll
     for (int j = 0; j < kStagePerThread; ++j) {
       const int item = tid + j * kFusedThreads;
       const int row = item / 8, piece = item % 8;
       const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
-      const int b = s * span + bl;
-      const bool live = s < splits && item < kStageItems && p < count && bl < span && b < B;
-      const int cell = sh.pair_token[live ? p : 0] * B + (live ? b : 0);
-      held[j] = live ? load_uint4_at(a.digits, static_cast<uint32_t>((cell * 3 + d) * 128 + 16 * piece))
-                     : make_uint4(0u, 0u, 0u, 0u);
+      const int cell = sh.pair_token[min(p, max(count, 1) - 1)] * B + min(s * span + bl, B - 1);
+      held[j] = load_uint4_at(a.digits, static_cast<uint32_t>((cell * 3 + d) * 128 + 16 * piece));
     }
+    const int b = min(s * span + min(sbl, span - 1), B - 1);
+    scale = load_uint2_at(stats, static_cast<uint32_t>((b * 4 * a.I + srow) * 2));
   };
-  auto stage_store = [&](int buffer, const uint4 *held) {
+  auto stage_store = [&](int buffer, const uint4 *held, uint2 scale) {
 #pragma unroll
     for (int j = 0; j < kStagePerThread; ++j) {
       const int item = tid + j * kFusedThreads;
-      if (item >= kStageItems) break;
       const int row = item / 8, piece = item % 8;
       const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
       *reinterpret_cast<uint4 *>(&sh.digits[buffer][bl][d][p][16 * piece]) = held[j];
     }
+    sh.scales[buffer][tid % kScaleEntries] = scale;
   };
   uint4 held[kStagePerThread];
+  uint2 held_scale;
 #pragma unroll
   for (int q = 0; q < kStageAhead; ++q) {
-    stage_load(q, held);
-    stage_store(q, held);
+    stage_load(q, held, held_scale);
+    stage_store(q, held, held_scale);
   }
   __syncthreads();
 
   float est[2][4] = {}, var[2][4] = {};
-  for (int s0 = 0; s0 < splits; s0 += 2)
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int s = s0 + h;
-    if (s >= splits) {
-      // (an odd split count: the last split's successor loads are read here,
-      // so no path round the loop leaves them in flight)
-#pragma unroll
-      for (int bl = 0; bl < kMaxSpan; ++bl)
-#pragma unroll
-        for (int up = 0; up < 2; ++up) consume(step[1][bl][up]);
-      break;
-    }
+  for (int s = 0; s < splits; ++s) {
     const int buffer = s % kStageBuffers;
     // split s + kStageAhead's digits go to the buffer split s - 1 used, which
     // every wave finished before the last barrier
-    stage_load(s + kStageAhead, held);
-    // split s + 1's steps (a repeat of split s's past the last)
-#pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl)
-#pragma unroll
-      for (int up = 0; up < 2; ++up) step[h ^ 1][bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);
+    stage_load(s + kStageAhead, held, held_scale);
     float part[2][4] = {}, vpart[2][4] = {};
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
       const int b = s * span + bl;
       const bool live_block = bl < span && b < B;
       const int qsum = sh.qsum[min(b, B - 1)][pp], shift = sh.shift[min(b, B - 1)][pp];
-      const float n2 = sh.norm2[min(b, B - 1)][pp];
-      const v4i start = v4i{-qsum, -qsum, -qsum, -qsum};
+      const float n2 = kGh5 ? sh.norm2[kGh5 ? min(b, B - 1) : 0][pp] : 0.0f;
+      const int start = -qsum;
       auto operand = [&](int h, int d) {
         return *reinterpret_cast<const v4i *>(&sh.digits[buffer][bl][d][pp][64 * h + k0]);
       };
-      // gate and up row tiles share each B operand read
-      const StepLoads *l = step[h][bl];
+      // gate and up row tiles share each B operand read; the expanded step's
+      // registers take its successor (a repeat past the last split)
       v4i a0[2], a1[2];
 #pragma unroll
       for (int up = 0; up < 2; ++up) {
-        a0[up] = expand_digits(l[up].words.x);
-        a1[up] = expand_digits(l[up].words.y);
+        a0[up] = expand_digits(step[bl][up].x);
+        a1[up] = expand_digits(step[bl][up].y);
+        // (the successor load stays below the expansion, so it can take the
+        // step's own registers: no copy round the loop waits for it)
+        asm volatile("" ::"v"(a0[up]), "v"(a1[up]) : "memory");
+        step[bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);
       }
       if (!live_block) continue;
       v4i acc[2];
       digit_dots(a0, a1, start, operand, acc);
 #pragma unroll
-      for (int up = 0; up < 2; ++up)
+      for (int up = 0; up < 2; ++up) {
+        const int entry = 32 * bl + 16 * up + 4 * wave + (lane >> 4);
+        const uint2 scale = sh.scales[buffer][entry];
+        const uint2 residual = kGh5 ? sh.scales[buffer][64 + entry] : make_uint2(0u, 0u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int sum = acc[up][r];
           const float dot = ldexpf(static_cast<float>(sum), -shift);
-          const uint32_t sw = r < 2 ? l[up].scale.x : l[up].scale.y;
+          const uint32_t sw = r < 2 ? scale.x : scale.y;
           part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);
           if (kGh5) {
-            const uint32_t rw = r < 2 ? l[up].residual.x : l[up].residual.y;
+            const uint32_t rw = r < 2 ? residual.x : residual.y;
             vpart[up][r] = fmaf(half_at(rw, r & 1), n2, vpart[up][r]);
           }
         }
+      }
     }
 #pragma unroll
     for (int up = 0; up < 2; ++up)
@@ -1298,7 +1312,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         if (kGh5) var[up][r] = s == 0 ? vpart[up][r] : var[up][r] + vpart[up][r];
       }
     if (s + 1 < splits) {
-      stage_store((s + kStageAhead) % kStageBuffers, held);
+      stage_store((s + kStageAhead) % kStageBuffers, held, held_scale);
       __syncthreads();
     }
   }
@@ -2151,8 +2165,6 @@ struct DownArgs {
 };
 
 constexpr int kDownOutputs = 8;  // outputs per down thread (H / 8 threads)
-
-typedef int32_t i32x8 __attribute__((ext_vector_type(8)));
 
 // The slot of a token's down tile: the slot whose tiles hold it, the tile's
 // first position in the slot's kept list, and the slot's count, expert and
