@@ -1192,21 +1192,31 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
     for (int up = 0; up < 2; ++up) step[bl][up] = load_step(0, bl, up);
 
-  // ---- the tile's pairs and per-(block, pair) constants
+  // ---- the tile's pairs (through the scalar cache: the tile list is an
+  // earlier launch's output) and per-(block, pair) constants
   if (tid < kPairTile) {
-    const int pair = tid < count ? a.group_pairs[kGroupPairs * z + tid] : 0;
+    const i32x8 lo = load_uniform(reinterpret_cast<const i32x8 *>(a.group_pairs + kGroupPairs * z));
+    const i32x8 hi = load_uniform(reinterpret_cast<const i32x8 *>(a.group_pairs + kGroupPairs * z + 8));
+    int pair = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      pair = tid == q ? lo[q] : pair;
+      pair = tid == q + 8 ? hi[q] : pair;
+    }
+    pair = tid < count ? pair : 0;
     sh.pair_token[tid] = pair / a.K;
     sh.pair_slot[tid] = pair % a.K;
   }
   __syncthreads();
-  for (int i = tid; i < B * kPairTile; i += kFusedThreads) {
-    const int b = i / kPairTile, p = i % kPairTile;
-    const bool live = p < count;
-    const long cell = live ? static_cast<long>(sh.pair_token[p]) * B + b : 0;
-    sh.qsum[b][p] = live ? a.qsums[cell] : 0;
-    sh.shift[b][p] = live ? a.qexp[cell] : 0;
-    if (kGh5) sh.norm2[kGh5 ? b : 0][p] = live ? a.norm2[cell] : 0.0f;
-  }
+  // thread tid's (block, pair) entry: tid = 16 b + p (256 threads cover the
+  // 16 blocks); loaded with the first split's staging, stored after it
+  static_assert(kFusedThreads == 16 * kPairTile, "one table entry per thread");
+  const int tb = tid / kPairTile, tp = tid % kPairTile;
+  const bool table_live = tb < B && tp < count;
+  const int table_cell = table_live ? sh.pair_token[tp] * B + tb : 0;
+  const int qsum_value = load_global(a.qsums + table_cell);
+  const int shift_value = load_global(a.qexp + table_cell);
+  const float norm2_value = kGh5 ? load_global(a.norm2 + table_cell) : 0.0f;
   // staging of split s: rows (block, digit, pair) of 128 bytes, 16 bytes per
   // thread and item. Every load is unconditional and in bounds: a pair past
   // the count reads the tile's first pair (its MFMA B column feeds only that
@@ -1223,14 +1233,22 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   const int sk = kGh5 ? (tid >> 6) & 1 : 0, sbl = (tid >> 5) & 1, sup = (tid >> 4) & 1;
   const int stile = (sup ? CT : 0) + min(group * kFusedWaves + ((tid >> 2) & 3), CT - 1);
   const int srow = (sk ? 2 * a.I : 0) + kRowTile * stile + 4 * (tid & 3);
+  // each staging item's byte offset without its block term (fixed per thread)
+  int stage_offset[kStagePerThread];
+#pragma unroll
+  for (int j = 0; j < kStagePerThread; ++j) {
+    const int item = tid + j * kFusedThreads;
+    const int row = item / 8, piece = item % 8;
+    const int d = (row / kPairTile) % 3, p = row % kPairTile;
+    stage_offset[j] = sh.pair_token[min(p, max(count, 1) - 1)] * B * 384 + d * 128 + 16 * piece;
+  }
   auto stage_load = [&](int s, uint4 *held, uint2 &scale) {
 #pragma unroll
     for (int j = 0; j < kStagePerThread; ++j) {
       const int item = tid + j * kFusedThreads;
-      const int row = item / 8, piece = item % 8;
-      const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
-      const int cell = sh.pair_token[min(p, max(count, 1) - 1)] * B + min(s * span + bl, B - 1);
-      held[j] = load_uint4_at(a.digits, static_cast<uint32_t>((cell * 3 + d) * 128 + 16 * piece));
+      const int bl = item / (8 * 3 * kPairTile);
+      const int b = min(s * span + bl, B - 1);
+      held[j] = load_uint4_at(a.digits, static_cast<uint32_t>(stage_offset[j] + b * 384));
     }
     const int b = min(s * span + min(sbl, span - 1), B - 1);
     scale = load_uint2_at(stats, static_cast<uint32_t>((b * 4 * a.I + srow) * 2));
@@ -1247,11 +1265,15 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   };
   uint4 held[kStagePerThread];
   uint2 held_scale;
-#pragma unroll
-  for (int q = 0; q < kStageAhead; ++q) {
-    stage_load(q, held, held_scale);
-    stage_store(q, held, held_scale);
-  }
+  static_assert(kStageAhead == 1, "one split staged ahead");
+  stage_load(0, held, held_scale);
+  // (no store moves above this point: the table and staging loads are all
+  // issued before the first wait)
+  asm volatile("" ::: "memory");
+  sh.qsum[tb][tp] = table_live ? qsum_value : 0;
+  sh.shift[tb][tp] = table_live ? shift_value : 0;
+  if (kGh5) sh.norm2[kGh5 ? tb : 0][tp] = table_live ? norm2_value : 0.0f;
+  stage_store(0, held, held_scale);
   __syncthreads();
 
   float est[2][4] = {}, var[2][4] = {};
