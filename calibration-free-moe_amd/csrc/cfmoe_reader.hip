@@ -1253,14 +1253,13 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     const int b = min(s * span + min(sbl, span - 1), B - 1);
     scale = load_uint2_at(stats, static_cast<uint32_t>((b * 4 * a.I + srow) * 2));
   };
+  // (row (bl 3 + d) 16 + p of a buffer is item / 8: one base offset per
+  // thread, item j a constant past it)
   auto stage_store = [&](int buffer, const uint4 *held, uint2 scale) {
+    int8_t *rows = &sh.digits[buffer][0][0][0][0] + (tid / 8) * kDigitStride + 16 * (tid % 8);
 #pragma unroll
-    for (int j = 0; j < kStagePerThread; ++j) {
-      const int item = tid + j * kFusedThreads;
-      const int row = item / 8, piece = item % 8;
-      const int bl = row / (3 * kPairTile), d = (row / kPairTile) % 3, p = row % kPairTile;
-      *reinterpret_cast<uint4 *>(&sh.digits[buffer][bl][d][p][16 * piece]) = held[j];
-    }
+    for (int j = 0; j < kStagePerThread; ++j)
+      *reinterpret_cast<uint4 *>(rows + j * (kFusedThreads / 8) * kDigitStride) = held[j];
     sh.scales[buffer][tid % kScaleEntries] = scale;
   };
   uint4 held[kStagePerThread];
@@ -1282,7 +1281,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     // split s + kStageAhead's digits go to the buffer split s - 1 used, which
     // every wave finished before the last barrier
     stage_load(s + kStageAhead, held, held_scale);
-    float part[2][4] = {}, vpart[2][4] = {};
+    // (a split's first block starts the chains from zero as an fma operand)
+    float part[2][4], vpart[2][4];
 #pragma unroll
     for (int bl = 0; bl < kMaxSpan; ++bl) {
       const int b = s * span + bl;
@@ -1305,7 +1305,14 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         asm volatile("" ::"v"(a0[up]), "v"(a1[up]) : "memory");
         step[bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);
       }
-      if (!live_block) continue;
+      if (!live_block) {
+        if (bl == 0)
+#pragma unroll
+          for (int up = 0; up < 2; ++up)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) part[up][r] = vpart[up][r] = 0.0f;
+        continue;
+      }
       v4i acc[2];
       digit_dots(a0, a1, start, operand, acc);
 #pragma unroll
@@ -1318,10 +1325,10 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
           const int sum = acc[up][r];
           const float dot = ldexpf(static_cast<float>(sum), -shift);
           const uint32_t sw = r < 2 ? scale.x : scale.y;
-          part[up][r] = fmaf(dot, half_at(sw, r & 1), part[up][r]);
+          part[up][r] = fmaf(dot, half_at(sw, r & 1), bl == 0 ? 0.0f : part[up][r]);
           if (kGh5) {
             const uint32_t rw = r < 2 ? residual.x : residual.y;
-            vpart[up][r] = fmaf(half_at(rw, r & 1), n2, vpart[up][r]);
+            vpart[up][r] = fmaf(half_at(rw, r & 1), n2, bl == 0 ? 0.0f : vpart[up][r]);
           }
         }
       }
