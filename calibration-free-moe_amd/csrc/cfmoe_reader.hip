@@ -1557,14 +1557,15 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   // candidate order.
   const uint32_t cutoff = prefix;
   const int room = want;
-#pragma unroll
-  for (int j = 0; j < kKeys; ++j) key[j] &= mask;
-  int above_here = 0, tied_here = 0;
+  // bit j of the thread's masks: candidate first + j is above / at the cutoff
+  uint32_t above_bits = 0, tied_bits = 0;
 #pragma unroll
   for (int j = 0; j < kKeys; ++j) {
-    above_here += any && valid(j) && key[j] > cutoff;
-    tied_here += any && valid(j) && key[j] == cutoff;
+    const uint32_t k = key[j] & mask;
+    above_bits |= static_cast<uint32_t>(any && valid(j) && k > cutoff) << j;
+    tied_bits |= static_cast<uint32_t>(any && valid(j) && k == cutoff) << j;
   }
+  const int above_here = __builtin_popcount(above_bits), tied_here = __builtin_popcount(tied_bits);
   // exclusive prefix over threads (16-bit fields: at most N keys each), one
   // barrier: the wave totals have an array of their own
   const int packed_here = above_here | (tied_here << 16);
@@ -1579,40 +1580,35 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
     packed += w < wave ? v : 0;
   }
   const int kept_total = (packed_total & 0xffff) + min(packed_total >> 16, room);
-  int above_before = packed & 0xffff, tied_before = packed >> 16;
-  uint32_t kept_bits = 0;  // bit j: candidate first + j kept
-  // the slot of the current candidate and the next slot start at or after
-  // this thread's first candidate (no division per key)
-  int slot = first / a.I, next_slot = (first + a.I - 1) / a.I, boundary = next_slot * a.I;
-#pragma unroll
-  for (int j = 0; j < kKeys; ++j) {
-    if (!valid(j)) continue;
-    const int i = first + j;
-    // the first candidate of a slot: the kept ids before it start the slot
-    if (i == boundary) {
-      slot_start[next_slot] = any ? min(above_before + min(tied_before, room), a.F) : 0;
-      slot = next_slot++;
-      boundary += a.I;
-    }
-    bool keep = false;
-    if (any && key[j] > cutoff) {
-      keep = true;
-    } else if (any && key[j] == cutoff) {
-      keep = tied_before < room;
-      ++tied_before;
-    }
-    kept_bits |= static_cast<uint32_t>(keep) << j;
-    const int position = above_before + min(tied_before - (keep && key[j] == cutoff ? 1 : 0), room);
-    if (keep) {
-      if (key[j] > cutoff) ++above_before;
-      if (position < a.F) {
-        a.next_ids[static_cast<long>(t) * a.F + position] = i;
-        // the channel's bit for this pair in its tile's mask (OR: any order)
-        const int slot_tile = a.tile_masks ? slot_tiles[slot] : -1;
-        if (slot_tile >= 0)
-          atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
-                   1u << (slot_tile % kGroupPairs));
-      }
+  const int above_before = packed & 0xffff, tied_before = packed >> 16;
+  // the thread's kept keys: every key above the cutoff and its first ties
+  // while the ties before them leave room; kept keys take consecutive
+  // positions from `base`, the kept count before the thread
+  const int tied_keep = max(0, min(room - tied_before, tied_here));
+  uint32_t kept_tied = 0, rest = tied_bits;
+  for (int n = 0; n < tied_keep; ++n) {
+    kept_tied |= rest & (0u - rest);
+    rest &= rest - 1;
+  }
+  const uint32_t kept_bits = above_bits | kept_tied;  // bit j: candidate first + j kept
+  const int base = above_before + min(tied_before, room);
+  auto kept_below = [&](int j) { return __builtin_popcount(kept_bits & ((1u << j) - 1u)); };
+  // a slot's first candidate in the thread's run (at most one: I >= the run):
+  // the kept ids before it start the slot
+  const int slot0 = first / a.I, jb = (slot0 + 1) * a.I - first;
+  if (first % a.I == 0 && valid(0)) slot_start[slot0] = any ? min(base, a.F) : 0;
+  if (jb < per && first + jb < a.N) slot_start[slot0 + 1] = any ? min(base + kept_below(jb), a.F) : 0;
+  for (uint32_t m = kept_bits; m; m &= m - 1) {
+    const int j = __builtin_ctz(m);
+    const int i = first + j, position = base + kept_below(j);
+    if (position < a.F) {
+      a.next_ids[static_cast<long>(t) * a.F + position] = i;
+      // the channel's bit for this pair in its tile's mask (OR: any order)
+      const int slot = j < jb ? slot0 : slot0 + 1;
+      const int slot_tile = a.tile_masks ? slot_tiles[slot] : -1;
+      if (slot_tile >= 0)
+        atomicOr(&a.tile_masks[static_cast<long>(slot_tile / kGroupPairs) * a.I + (i - slot * a.I)],
+                 1u << (slot_tile % kGroupPairs));
     }
   }
   // the run's selected flags (and cleared completed flags) as one store per
