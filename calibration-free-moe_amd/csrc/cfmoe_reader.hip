@@ -1774,7 +1774,9 @@ __device__ __forceinline__ void encode_tile_direct(const Args &a, int tile, int 
   constexpr int R = kDirectRank;
   const int lane = threadIdx.x & 63;
   const int c = tile * 64 + lane;
-  const int e = __builtin_amdgcn_readfirstlane(load_global(a.ids + t * a.K + k));
+  // the slot's expert through the scalar cache (the ids are an earlier
+  // launch's output): the flag and value loads below do not wait for it
+  const int e = load_uniform(a.ids + t * a.K + k);
   const bool local = is_active(a.padding, t) && e >= 0;
   // the tile's flags and values through buffer resources (one lane offset;
   // channels past I read zeros and are not skipped)
