@@ -354,9 +354,13 @@ constexpr int kMaxPairs = 8192;    // T * K routed pairs grouped per call
 constexpr int kWorkspaceBuffers = 31;  // cfmoe_workspace pointers after capacity
 constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column block)
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
+// Prepare workgroups: 256 threads, or 1024 from kWidePreparePairs routed
+// pairs (the routing workgroup, alone on its CU, is the launch's longest: at
+// 2048 pairs 1024 threads take it from 16.8 to 11.7 us; below 1024 pairs the
+// narrower cell workgroups spread the rotations over more CUs).
 constexpr int kPrepareThreads = 256;
-
-constexpr int kPrepareWaves = kPrepareThreads / 64;
+constexpr int kWidePrepareThreads = 1024;
+constexpr int kWidePreparePairs = 1024;
 
 // LDS of the routing block, carved from the launch's dynamic LDS, which the
 // host sizes for the call's pairs and experts (route_lds_bytes): the pairs'
@@ -366,13 +370,13 @@ constexpr int kPrepareWaves = kPrepareThreads / 64;
 struct RouteShared {
   int16_t *sorted, *routed;
   int *counts, *base;
-  int16_t *wave_counts;  // [kPrepareWaves][experts]
+  int16_t *wave_counts;  // [waves][experts]
 };
 
 __host__ __device__ inline long route_pairs_padded(int pairs) { return (pairs + 7) / 8 * 8; }
 
-__host__ __device__ inline long route_lds_bytes(int pairs, int experts) {
-  return 2 * 2 * route_pairs_padded(pairs) + 2 * 4 * (experts + 1) + 2 * kPrepareWaves * experts;
+__host__ __device__ inline long route_lds_bytes(int pairs, int experts, int waves) {
+  return 2 * 2 * route_pairs_padded(pairs) + 2 * 4 * (experts + 1) + 2L * waves * experts;
 }
 
 __device__ inline RouteShared route_layout(char *lds, int pairs, int experts) {
@@ -386,9 +390,10 @@ __device__ inline RouteShared route_layout(char *lds, int pairs, int experts) {
   return r;
 }
 
-template <bool kIds64, bool kWeights16>
+template <int kPrepareThreads, bool kIds64, bool kWeights16>
 __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const RouteShared &shared,
                                                 int *scratch) {
+  constexpr int kPrepareWaves = kPrepareThreads / 64;
   int16_t *sorted = shared.sorted;
   int16_t *routed = shared.routed;
   int *counts = shared.counts, *base = shared.base;
@@ -567,27 +572,29 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   }
 }
 
+template <int kPrepareThreads>
 __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
+  constexpr int kPrepareWaves = kPrepareThreads / 64;
   // block 0 routes and groups (the longest block, dispatched first)
   extern __shared__ __align__(16) char route_lds[];
   __shared__ int route_scratch[32];
   if (a.route && blockIdx.x == 0) {
     const RouteShared shared = route_layout(route_lds, a.T * a.K, a.E);
     if (a.flags & CFMOE_IDS_INT64) {
-      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<true, true>(a, shared, route_scratch);
-      else route_and_group<true, false>(a, shared, route_scratch);
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<kPrepareThreads, true, true>(a, shared, route_scratch);
+      else route_and_group<kPrepareThreads, true, false>(a, shared, route_scratch);
     } else {
-      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<false, true>(a, shared, route_scratch);
-      else route_and_group<false, false>(a, shared, route_scratch);
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<kPrepareThreads, false, true>(a, shared, route_scratch);
+      else route_and_group<kPrepareThreads, false, false>(a, shared, route_scratch);
     }
     return;
   }
   const int cell_block = static_cast<int>(blockIdx.x) - (a.route ? 1 : 0);
-  __shared__ float compact_all[4][128];
+  __shared__ float compact_all[kPrepareWaves][128];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   // waves past the last cell still reach the block barrier below
-  const int cell_id = min(cell_block * 4 + wave, a.cells - 1);
-  const bool owner = cell_block * 4 + wave < a.cells;
+  const int cell_id = min(cell_block * kPrepareWaves + wave, a.cells - 1);
+  const bool owner = cell_block * kPrepareWaves + wave < a.cells;
   const int B = a.H / 128;
   const int t = cell_id / B, b = cell_id % B;
   float *compact = compact_all[wave];
@@ -2655,10 +2662,18 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.route = route;
   a.rotate = rotate;
   a.cells = tokens * (rotate ? s.B : 1);
-  const int cell_blocks = (a.cells + 3) / 4;
-  const long lds = route ? route_lds_bytes(tokens * s.K, d->experts) : 0;
-  hipLaunchKernelGGL(prepare_kernel, dim3(cell_blocks + (route ? 1 : 0)), dim3(kPrepareThreads),
-                     static_cast<unsigned>(lds), stream, a);
+  const int pairs = tokens * s.K;
+  const bool wide = route && pairs >= kWidePreparePairs &&
+                    route_lds_bytes(pairs, d->experts, kWidePrepareThreads / 64) <= 96 * 1024;
+  const int threads = wide ? kWidePrepareThreads : kPrepareThreads;
+  const int cell_blocks = (a.cells + threads / 64 - 1) / (threads / 64);
+  const long lds = route ? route_lds_bytes(pairs, d->experts, threads / 64) : 0;
+  if (wide)
+    hipLaunchKernelGGL(prepare_kernel<kWidePrepareThreads>, dim3(cell_blocks + 1), dim3(threads),
+                       static_cast<unsigned>(lds), stream, a);
+  else
+    hipLaunchKernelGGL(prepare_kernel<kPrepareThreads>, dim3(cell_blocks + (route ? 1 : 0)), dim3(threads),
+                       static_cast<unsigned>(lds), stream, a);
   return check_launch("prepare");
 }
 
@@ -3073,7 +3088,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.R = s.R;
   op.max_tiles = s.max_tiles;
   op.encoder_tiles = s.encoder_tiles;
-  op.columns = grouped && s.K <= 16 ? 256 : 64;  // LDS <= 16 KB
+  // wider workgroups fold each token's encoder tiles fewer times: 512 outputs
+  // from 128 tokens (c3 at 128 tokens: 18.4 -> 14.6 us), 256 from the grouped
+  // size, 64 below it; LDS K x columns x 4 <= 16 KB
+  op.columns = !grouped ? 64 : s.K <= 8 && tokens >= 128 ? 512 : s.K <= 16 ? 256 : 64;
   hipLaunchKernelGGL(output_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
                      dim3(kOutputThreads), static_cast<unsigned>(s.K * op.columns * sizeof(float)),
                      stream, op);
