@@ -13,7 +13,7 @@ import os
 LIBRARY_NAME = "libcfmoe_reader.so"
 LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIBRARY_NAME)
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 POINT = 1
 GELU = 2
@@ -57,6 +57,7 @@ class WeightPointers(ctypes.Structure):
         ("signs", ctypes.c_void_p),
         ("threshold", ctypes.c_void_p),
         ("trit_planes", ctypes.c_void_p),
+        ("encoder_tiles", ctypes.c_void_p),
     ]
 
 

@@ -73,6 +73,8 @@ SelectionScore = Literal["recovery-aware", "point"]
 DOWN_TILE = 32
 REFERENCE_DOWN_TILE = 128
 ENCODER_TILE = 64
+# Recovery rank whose encoder runs inside the exact launch (tile-major coefficients).
+DIRECT_RANK = 32
 
 
 def aligned_pairs(pairs: int, experts: int) -> int:
@@ -494,6 +496,7 @@ class ProgressiveReader:
         self.native_gu = gate_up.detach()
         self.down = down.detach()
         self.encoder: Tensor | None = None
+        self._encoder_tiles: Tensor | None = None
         self.decoder: Tensor | None = None
         self.recovery_geometry: Tensor | None = None
         prepared = False
@@ -502,6 +505,17 @@ class ProgressiveReader:
                 encoder.to(device=device, dtype=torch.bfloat16).transpose(1, 2).contiguous()
             )
             self.decoder = decoder.to(device=device, dtype=torch.bfloat16).contiguous()
+            if self.encoder.shape[2] == DIRECT_RANK:
+                # the exact launch's encoder reads each rank's 64 coefficients of
+                # a 64-channel tile as one contiguous row: [E, tiles, R, 64]
+                tiles = ceil(i / ENCODER_TILE)
+                padded = torch.zeros(
+                    (e, tiles * ENCODER_TILE, DIRECT_RANK), dtype=torch.bfloat16, device=device
+                )
+                padded[:, :i] = self.encoder
+                self._encoder_tiles = (
+                    padded.view(e, tiles, ENCODER_TILE, DIRECT_RANK).transpose(2, 3).contiguous()
+                )
             if selection_score != "point":
                 prepared = True
                 self.recovery_geometry = self._geometry(down)
@@ -595,6 +609,7 @@ class ProgressiveReader:
             _pointer(self.sketch_signs),
             _pointer(self.selection_threshold),
             _pointer(self.sketch_trit_planes),
+            _pointer(self._encoder_tiles),
         )
         self._workspace_c = workspace.pointers(self.read_work)
         self._workspace_c.next_ids = _pointer(self.candidate_ids[1])

@@ -1691,6 +1691,7 @@ __global__ void select_all_kernel(SelectArgs a) {
 
 struct EncodeArgs {
   const uint16_t *encoder_t;
+  const uint16_t *encoder_tiles;  // [E, tiles, R, 64] (R = kDirectRank) or NULL
   const float *partial;
   const uint16_t *activations;
   const uint8_t *completed;
@@ -1698,7 +1699,7 @@ struct EncodeArgs {
   const int32_t *ids;
   const uint8_t *padding;
   float *parts;
-  int I, K, N, R, tiles, gelu;
+  int I, K, N, R, tiles, gelu, E;
 };
 
 constexpr int kEncodeStride = 72;  // LDS row stride (bf16) of a staged encoder row
@@ -1769,71 +1770,87 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
   encode_tile(a, blockIdx.x, blockIdx.y, blockIdx.z, true, coefficients, kEncodeStride);
 }
 
-// The same item without LDS, at R = kDirectRank: lane r + 32 h (h = 0, 1)
-// loads the coefficients E[32 h + i][r] (i < 32) at once (row offsets are
-// immediates); lanes r < 32 run the chain over the tile's first 32 channels,
-// lanes 32 + r continue it over the last 32 from lane r's sum. Same order and
-// roundings as encode_tile.
+// Two (64-channel tile, slot, token) items on one wave at R = kDirectRank:
+// item q = tile + tiles (k + K t) of the flat item order, the wave's pair
+// 2 p and 2 p + 1 (the second may be past `items`: its half stores nothing).
+// Lane 32 h + r takes rank r of item 2 p + h and runs its whole chain over
+// the tile's 64 channels in order. Lanes 32 h + j and 32 h + 32 + j first
+// form item h's values of channels j and 32 + j (zero for a kept channel, a
+// channel past I or a slot with no local expert: fma(0, b, acc) == acc
+// exactly for finite b, since the chain starts at +0 and never holds -0, so
+// a zero value leaves the chain as skipping it would) and put them in LDS,
+// from where every step reads four values of its half's item at once
+// (broadcast reads). The coefficients E[c][r] arrive packed two to a word.
+// Same order and roundings as encode_tile.
 constexpr int kDirectRank = 32;
 
 template <class Args>  // EncodeArgs, or the grouped exact launch's arguments
-__device__ __forceinline__ void encode_tile_direct(const Args &a, int tile, int k, int t) {
+__device__ __forceinline__ void encode_pair_direct(const Args &a, int p, int items, int t_base) {
   constexpr int R = kDirectRank;
+  __shared__ __align__(16) float channel_values[2][64];
   const int lane = threadIdx.x & 63;
-  const int c = tile * 64 + lane;
-  // the slot's expert through the scalar cache (the ids are an earlier
-  // launch's output): the flag and value loads below do not wait for it
-  const int e = load_uniform(a.ids + t * a.K + k);
-  const bool local = is_active(a.padding, t) && e >= 0;
-  // the tile's flags and values through buffer resources (one lane offset;
-  // channels past I read zeros and are not skipped)
-  const int rows = min(64, a.I - tile * 64);
+  const int h = lane >> 5, r = lane & 31;
+  const int q = min(2 * p + h, items - 1);
+  const bool store = 2 * p + h < items;
+  const int tile = q % a.tiles, rest = q / a.tiles;
+  const int k = rest % a.K, t = t_base + rest / a.K;
+  // the item's expert (lanes of a half agree); the flag and value loads
+  // below do not wait for it
+  const int e = load_global(a.ids + t * a.K + k);
+  const bool active = is_active(a.padding, t);
+  // the item's flags and values of channels r and 32 + r
   const long flat = static_cast<long>(t) * a.N + static_cast<long>(k) * a.I + tile * 64;
   const long base = static_cast<long>(t) * 2 * a.N + static_cast<long>(k) * a.I + tile * 64;
-  const uint8_t is_selected =
-      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.selected + flat, rows), lane, 0, 0);
-  const uint8_t is_completed =
-      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.completed + flat, rows), lane, 0, 0);
-  const uint16_t exact = __builtin_amdgcn_raw_buffer_load_b16(
-      buffer_resource(a.activations + flat, 2 * rows), 2 * lane, 0, 0);
-  const float gate = __uint_as_float(
-      __builtin_amdgcn_raw_buffer_load_b32(buffer_resource(a.partial + base, 4 * rows), 4 * lane, 0, 0));
-  const float up = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-      buffer_resource(a.partial + base + a.N, 4 * rows), 4 * lane, 0, 0));
-  // the tile's rows of E (rows past I read zeros)
-  const int r = lane & 31, half = lane >> 5;
-  // (an absent slot's resource is empty: its loads read zeros, request nothing)
-  const __amdgpu_buffer_rsrc_t block = buffer_resource(
-      a.encoder_t + (static_cast<long>(local ? e : 0) * a.I + tile * 64) * R, local ? rows * R * 2 : 0);
-  uint16_t coefficient[32];
+  uint8_t is_selected[2], is_completed[2];
+  uint16_t exact[2];
+  float gate[2], up[2];
 #pragma unroll
-  for (int i = 0; i < 32; ++i)
-    coefficient[i] = __builtin_amdgcn_raw_buffer_load_b16(block, 2 * (32 * half * R + r) + 2 * i * R, 0, 0);
-  const int skip = c < a.I && !is_selected;
-  float v = 0.0f;
-  if (skip)
-    v = is_completed ? bf16f(exact) : bfr(cfm_activate(bfr(gate), a.gelu != 0) * bfr(up));
-  const uint64_t skipped = __ballot(skip);
-  // each step tests its bit of the skipped mask in place (the empty asm keeps
-  // the compiler from precomputing all 32 conditions into scalar registers)
-  uint32_t low = static_cast<uint32_t>(skipped), high = static_cast<uint32_t>(skipped >> 32);
+  for (int s = 0; s < 2; ++s) {
+    const int j = 32 * s + r;
+    const bool inside = tile * 64 + j < a.I;
+    const long at = inside ? j : 0;
+    is_selected[s] = inside ? a.selected[flat + at] : 1;
+    is_completed[s] = a.completed[flat + at];
+    exact[s] = a.activations[flat + at];
+    gate[s] = a.partial[base + at];
+    up[s] = a.partial[base + a.N + at];
+  }
+  const bool local = active && e >= 0;
+  // coefficients E[tile 64 + c][r], c < 64: rank r's contiguous 128-byte row
+  // of the tile-major copy, two channels to a word (channels past I are zero;
+  // an absent slot reads expert 0's, which meet only zero values)
+  const __amdgpu_buffer_rsrc_t coefficients = buffer_resource(
+      a.encoder_tiles, static_cast<int>(static_cast<long>(a.E) * a.tiles * R * 64 * 2));
+  const int row = ((max(e, 0) * a.tiles + tile) * R + r) * 128;
+  uint32_t coefficient[32];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) {
+    const uint4 w = buffer_load16(coefficients, row + 16 * m);
+    coefficient[4 * m] = w.x;
+    coefficient[4 * m + 1] = w.y;
+    coefficient[4 * m + 2] = w.z;
+    coefficient[4 * m + 3] = w.w;
+  }
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const bool skip = local && !is_selected[s];
+    float value = 0.0f;
+    if (skip)
+      value = is_completed[s] ? bf16f(exact[s]) : bfr(cfm_activate(bfr(gate[s]), a.gelu != 0) * bfr(up[s]));
+    channel_values[h][32 * s + r] = value;
+  }
+  __syncthreads();  // one-wave workgroups: orders the LDS writes before the reads
+  const float4 *values = reinterpret_cast<const float4 *>(channel_values[h]);
   float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    asm volatile("" : "+s"(low));
-    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
-    const float next = fmaf(value, local ? bf16f(coefficient[i]) : 0.0f, acc);
-    acc = (low >> i) & 1u ? next : acc;
+  for (int g = 0; g < 16; ++g) {
+    const float4 v = values[g];
+    acc = fmaf(v.x, __uint_as_float(coefficient[2 * g] << 16), acc);
+    acc = fmaf(v.y, __uint_as_float(coefficient[2 * g] & 0xffff0000u), acc);
+    acc = fmaf(v.z, __uint_as_float(coefficient[2 * g + 1] << 16), acc);
+    acc = fmaf(v.w, __uint_as_float(coefficient[2 * g + 1] & 0xffff0000u), acc);
   }
-  acc = __shfl(acc, r);
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    asm volatile("" : "+s"(high));
-    const float value = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32 + i));
-    const float next = fmaf(value, local ? bf16f(coefficient[i]) : 0.0f, acc);
-    acc = (high >> i) & 1u ? next : acc;
-  }
-  if (half == 1) a.parts[((static_cast<long>(t) * a.K + k) * a.tiles + tile) * R + r] = acc;
+  if (store) a.parts[(static_cast<long>(t_base) * a.K * a.tiles + q) * R + r] = acc;
 }
 
 // Grouped exact rows (batches of grouped_tokens or more, as
@@ -1867,8 +1884,9 @@ struct GroupExactArgs {
   int dense;  // every channel kept by every pair (no tile masks)
   // recovery encoder items (R = kDirectRank) run past the exact tiles
   const uint16_t *encoder_t;
+  const uint16_t *encoder_tiles;
   float *parts;  // encoder partials
-  int tiles, encode_items;
+  int tiles, encode_items, E;
   // the down kernel's workgroup order, built by the first kDownBuilders
   // workgroups (or NULL): list of down_blocks items, then per-builder slot
   // records (two words each) from word order_words, slot_capacity per builder
@@ -2061,14 +2079,14 @@ __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, i
   }
   if (block < a.tile_items) return block;
   const int item = block - a.tile_items;
-  if (item < a.encode_items) {
-    // recovery encoder item (tile, slot, token), tile fastest; it reads no
-    // exact result (a skipped channel is never completed)
-    const int tile = item % a.tiles, rest = item / a.tiles;
-    encode_tile_direct(a, tile, rest % a.K, rest / a.K);
+  const int encode_blocks = (a.encode_items + 1) / 2;
+  if (item < encode_blocks) {
+    // two recovery encoder items (tile, slot, token), tile fastest; they read
+    // no exact result (a skipped channel is never completed)
+    encode_pair_direct(a, item, a.encode_items, 0);
     return -1;
   }
-  const int t = item - a.encode_items;
+  const int t = item - encode_blocks;
   if (t >= a.T) return -1;
   const bool active = is_active(a.padding, t);
   for (int k = 0; k < a.K; ++k) {
@@ -2344,8 +2362,7 @@ __global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
   const int t = blockIdx.y;
   if (static_cast<int>(blockIdx.x) >= a.exact_blocks) {
     const int item = blockIdx.x - a.exact_blocks;  // (tile, slot), tile fastest
-    if (item < a.encode_items)
-      encode_tile_direct(a.encode, item % a.encode.tiles, item / a.encode.tiles, t);
+    if (2 * item < a.encode_items) encode_pair_direct(a.encode, item, a.encode_items, t);
     return;
   }
   const int f = blockIdx.x;
@@ -2786,6 +2803,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   if (tokens * s.K > kMaxPairs) return fail(CFMOE_EINVAL, "tokens * top_k exceeds 8192 pairs");
   if (s.R > 0 && (!weights->encoder_t || !weights->decoder))
     return fail(CFMOE_EINVAL, "rank > 0 needs encoder and decoder");
+  if (s.R == kDirectRank && (!weights->encoder_tiles || reinterpret_cast<uintptr_t>(weights->encoder_tiles) % 16))
+    return fail(CFMOE_EINVAL, "encoder_tiles (16-byte aligned) is required at rank 32");
   if ((dims->flags & CFMOE_THRESHOLD) && !weights->threshold)
     return fail(CFMOE_EINVAL, "threshold flag without threshold");
   if (s.screened && (!weights->trit_planes || reinterpret_cast<uintptr_t>(weights->trit_planes) % 8))
@@ -2941,6 +2960,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   EncodeArgs en;
   memset(&en, 0, sizeof(en));
   en.encoder_t = static_cast<const uint16_t *>(weights->encoder_t);
+  en.encoder_tiles = static_cast<const uint16_t *>(weights->encoder_tiles);
+  en.E = dims->experts;
   en.partial = workspace->partial;
   en.activations = static_cast<const uint16_t *>(workspace->activations);
   en.completed = workspace->completed;
@@ -2996,6 +3017,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     gx.channel_groups = (s.I + kExactChannels - 1) / kExactChannels;
     gx.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * gx.channel_groups;
     gx.encoder_t = en.encoder_t;
+    gx.encoder_tiles = en.encoder_tiles;
+    gx.E = en.E;
     gx.parts = en.parts;
     gx.tiles = en.tiles;
     gx.encode_items = encode_items * tokens;
@@ -3010,7 +3033,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     gx.union_row_bytes = 4.0 * s.H;
     const int counters = gx.read_work ? kUnionCounters : 0;
     hipLaunchKernelGGL(group_exact_kernel,
-                       dim3(kDownBuilders + counters + gx.tile_items + gx.encode_items + tokens),
+                       dim3(kDownBuilders + counters + gx.tile_items + (gx.encode_items + 1) / 2 + tokens),
                        dim3(64 * kGroupExactWaves), 0, stream, gx);
     if ((rc = check_launch("exact"))) return rc;
   } else if (stages & (1u << CFMOE_STAGE_EXACT)) {
@@ -3032,7 +3055,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     ex.encode = en;
     ex.exact_blocks = s.F;
     ex.encode_items = encode_items;
-    hipLaunchKernelGGL(exact_kernel, dim3(s.F + encode_items, tokens), dim3(kWave), 0, stream, ex);
+    hipLaunchKernelGGL(exact_kernel, dim3(s.F + (encode_items + 1) / 2, tokens), dim3(kWave), 0, stream, ex);
     if ((rc = check_launch("exact"))) return rc;
   }
 

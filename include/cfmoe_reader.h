@@ -36,7 +36,7 @@ extern "C" {
 
 typedef struct ihipStream_t *cfmoe_stream;
 
-#define CFMOE_ABI_VERSION 9
+#define CFMOE_ABI_VERSION 10
 
 /* cfmoe_dims.flags */
 #define CFMOE_POINT 1u          /* point score (else five-node Gauss-Hermite) */
@@ -94,6 +94,9 @@ typedef struct cfmoe_weights {
   const int8_t *signs;     /* [H] rotation signs */
   const float *threshold;  /* [1] selection threshold or NULL */
   const uint32_t *trit_planes; /* screen layout of `codes` (cfmoe_pack_trit_planes) */
+  const void *encoder_tiles;   /* bf16 [E, ceil(I/64), R, 64]: encoder_t tile-major, channels past
+                                  I zero; required at R == 32 (the exact launch's encoder), else
+                                  unused */
 } cfmoe_weights;
 
 /* Caller-allocated scratch, sized for `capacity` tokens (sizes in bytes from
