@@ -932,7 +932,9 @@ class ProgressiveReader:
         point = self.selection_score == "point"
         splits = _screen_splits(h)
         planes = 1 + (not point)
-        split_io = float(16 * splits * n * planes) * (splits > 1) * screened
+        # both screens reduce their block splits on chip (registers, or LDS
+        # inside one workgroup): no split partial crosses HBM
+        split_io = 0.0
         split_adds = float(2 * (splits - 1) * n * planes) * screened
         return {
             "charged_bytes": charged,
@@ -972,11 +974,11 @@ class ProgressiveReader:
             * input_sparse,
             "screen_mask_arithmetic_per_token": float(h // 128 * 9 * 128) * input_sparse,
             "screen_compaction_scan_adds_per_token": float(h // 128 * 127) * input_sparse,
-            # The one (expert-major) screen runs at every batch size: each
-            # split's FP32 partials are written and read back once; there are
-            # no arrival counters. Its workgroups stage the tile's kept grid
-            # values and coordinates (8 B each) once per range of row tiles,
-            # at most ceil(2 I / 64) ranges.
+            # The expert-major screen runs at every batch size and sums each
+            # row's block splits in order on chip; there are no arrival
+            # counters. Its workgroups read each pair's three 128-byte digit
+            # planes per block once per workgroup of the pair's tile: I / 16
+            # workgroups per tile below the grouped size, I / 64 from it.
             "batch_one_screen_split_io_bytes": split_io,
             "batched_screen_split_io_bytes_per_token": split_io,
             "batched_screen_split_adds_per_token": split_adds,
@@ -987,7 +989,7 @@ class ProgressiveReader:
             "grouped_screen_split_io_bytes_per_token": split_io,
             "grouped_screen_split_adds_per_token": split_adds,
             "grouped_screen_union_io_bytes_per_token_upper_bound": float(
-                8 * k * (h // 128) * p.screen_coordinates * -(-2 * i // 64)
+                384 * k * (h // 128) * -(-i // 64)
             )
             * screened,
             "per_token_screen_dot_terms": float(
