@@ -2107,35 +2107,54 @@ group_exact_kernel(GroupExactArgs a) {
   if (block < 0) return;
   const int z = block / a.channel_groups;
   const int c0 = (block % a.channel_groups) * kExactChannels;
-  // The tile count, the tile's expert, pair count and 16 pair slots through
-  // the scalar cache, and lane l < 16 the mask of channel c0 + l, in one
-  // round trip: z < tile bound <= T * K keeps every address in bounds
-  // whatever the tile count, and only slots named by mask bits (< count) are
-  // used.
+  // An expert's tiles are consecutive. An even tile whose successor has the
+  // same expert takes both tiles' pairs (32 pair slots, contiguous), so the
+  // expert's rows are read once per two tiles; the odd tile's item then has
+  // nothing to do. The tile count, both tiles' experts, pair counts and pair
+  // slots through the scalar cache, and lane l < 4 the mask of channel
+  // c0 + l % 2 in tile z + l / 2, in one round trip: z + 1 < tile bound <=
+  // T * K keeps every address in bounds whatever the tile count, and only
+  // slots named by mask bits (< count) are used.
+  const int bound = a.tile_items / a.channel_groups;
+  const int next_z = min(z + 1, bound - 1);
   const int total = load_uniform(a.group_total);
   const int e = load_uniform(a.group_experts + z);
   const int count = load_uniform(a.group_counts + z);
+  const int next_count = load_uniform(a.group_counts + next_z);
   const i32x16 slots = load_uniform(reinterpret_cast<const i32x16 *>(a.group_pairs + kGroupPairs * z));
+  const i32x16 next_slots =
+      load_uniform(reinterpret_cast<const i32x16 *>(a.group_pairs + kGroupPairs * next_z));
   const int lane_channel = c0 + (lane & (kExactChannels - 1));
-  const bool lane_in = lane < kExactChannels && lane_channel < a.I;
+  const int lane_tile = lane < kExactChannels ? z : next_z;
+  const bool lane_in = lane < 2 * kExactChannels && lane_channel < a.I;
   const uint32_t mask_word =
-      lane_in ? load_global(a.tile_masks + static_cast<long>(z) * a.I + lane_channel) : 0u;
+      lane_in ? load_global(a.tile_masks + static_cast<long>(lane_tile) * a.I + lane_channel) : 0u;
   // the neighbouring tiles' experts: an expert split into several tiles has
   // its rows read by each of them (entries past the count are never used)
-  const int bound = a.tile_items / a.channel_groups;
   const int before = load_uniform(a.group_experts + max(z - 1, 0));
-  const int after = load_uniform(a.group_experts + min(z + 1, bound - 1));
+  const int after = load_uniform(a.group_experts + next_z);
   // all issued before any is tested (else each waits under its branch)
-  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots), "s"(before), "s"(after));
+  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(next_count), "s"(slots), "s"(next_slots),
+               "s"(before), "s"(after));
   if (z >= total) return;
+  if ((z & 1) && before == e) return;  // the previous (even) tile's item holds this tile
+  const bool with_next = !(z & 1) && z + 1 < total && after == e;
   const bool shared_rows = (z > 0 && before == e) || (z + 1 < total && after == e);
-  // lane p < count: pair p of the tile
+  // lane p < 32: pair p of the two tiles (p >= 16: the next tile's p - 16)
   int pair = slots[0];
 #pragma unroll
   for (int p = 1; p < kGroupPairs; ++p) pair = (lane & (kGroupPairs - 1)) == p ? slots[p] : pair;
+  int next_pair = next_slots[0];
+#pragma unroll
+  for (int p = 1; p < kGroupPairs; ++p) next_pair = (lane & (kGroupPairs - 1)) == p ? next_slots[p] : next_pair;
+  pair = (lane & kGroupPairs) ? next_pair : pair;
   const int token = pair / a.K, pair_slot = pair % a.K;
-  // count <= 16
-  const uint32_t lane_mask = a.dense ? (lane_in ? (1u << count) - 1u : 0u) : mask_word;
+  // counts <= 16; lane l < kExactChannels: channel c0 + l's mask over both tiles
+  const uint32_t next_word = static_cast<uint32_t>(__shfl(static_cast<int>(mask_word), lane + kExactChannels));
+  const uint32_t own = a.dense ? (1u << count) - 1u : mask_word;
+  const uint32_t next_own = a.dense ? (1u << next_count) - 1u : next_word;
+  const bool lane_own = lane < kExactChannels && lane_channel < a.I;
+  const uint32_t lane_mask = !lane_own ? 0u : own | (with_next ? next_own << kGroupPairs : 0u);
   // the wave's channels that some pair kept, in order
   for (uint64_t kept = __ballot(lane_mask != 0u); kept; kept &= kept - 1) {
     const int at = __builtin_ctzll(kept);
@@ -2195,7 +2214,7 @@ group_exact_kernel(GroupExactArgs a) {
       kept_g = lane == pp ? g : kept_g;
       kept_u = lane == pp ? uu : kept_u;
     }
-    if (lane < kGroupPairs && ((mask >> lane) & 1u)) exact_results(a, token, logical, kept_g, kept_u);
+    if (lane < 2 * kGroupPairs && ((mask >> lane) & 1u)) exact_results(a, token, logical, kept_g, kept_u);
   }
 }
 
