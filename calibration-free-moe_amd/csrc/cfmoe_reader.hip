@@ -962,7 +962,6 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   extern __shared__ __align__(16) int8_t small_digits[];
   __shared__ float parts[kMaxSplits][2][64][4];
   __shared__ float vparts[kGh5 ? kMaxSplits : 1][2][64][4];
-  __shared__ int pair_token[kPairTile], pair_slot[kPairTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
     const int t = blockIdx.x - a.tile_items;
@@ -971,11 +970,24 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   }
   const int CT = a.I / kRowTile, RT = 2 * CT;
   const int z = blockIdx.x / CT, ct = blockIdx.x % CT;
-  if (z >= load_uniform(a.group_total)) return;
-  const int B = a.H / 128;
+  // the tile count, the tile's expert, pair count and 16 pair slots through
+  // the scalar cache in one round trip (z < tile bound <= T * K keeps every
+  // address in bounds whatever the count; slots past the count are unused)
+  const int total = load_uniform(a.group_total);
   const int e = load_uniform(a.group_experts + z);
   const int count = load_uniform(a.group_counts + z);
+  const i32x16 slots = load_uniform(reinterpret_cast<const i32x16 *>(a.group_pairs + kGroupPairs * z));
+  asm volatile("" ::"s"(total), "s"(e), "s"(count), "s"(slots));
+  if (z >= total) return;
+  const int B = a.H / 128;
   const int pp = lane % 16, k0 = 16 * (lane / 16), row_in_tile = 4 * (lane / 16);
+  // lane pp's pair (pairs past the count repeat the last one); lane p < 16
+  // holds pair p's token for the staging below
+  const int my_row = min(pp, count - 1);
+  int my_pair = slots[0];
+#pragma unroll
+  for (int p = 1; p < kPairTile; ++p) my_pair = my_row == p ? slots[p] : my_pair;
+  const int my_token = my_pair / a.K, my_slot = my_pair % a.K;
   const int span = a.span, splits = a.splits;
   const int per_wave = (splits + kSmallWaves - 1) / kSmallWaves;
   const int s_begin = wave * per_wave, s_end = min(splits, s_begin + per_wave);
@@ -998,18 +1010,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
         if (kGh5)
           step[si][j][up].residual = load_global(reinterpret_cast<const uint2 *>(plane + 2 * a.I));
       }
-  if (tid < kPairTile) {
-    const int pair = tid < count ? a.group_pairs[kGroupPairs * z + tid] : 0;
-    pair_token[tid] = pair / a.K;
-    pair_slot[tid] = pair % a.K;
-  }
-  __syncthreads();
   const bool live_pair = pp < count;
-  const long pair_cell = static_cast<long>(pair_token[min(pp, count - 1)]) * B;
+  const long pair_cell = static_cast<long>(my_token) * B;
   // the score's inputs (used by wave 0's live lanes) in this round trip
-  const ScoreInputs inputs = load_score_inputs(a, e, pair_token[min(pp, count - 1)],
-                                               pair_slot[min(pp, count - 1)],
-                                               kRowTile * ct + row_in_tile);
+  const ScoreInputs inputs = load_score_inputs(a, e, my_token, my_slot, kRowTile * ct + row_in_tile);
   // the lane's pair's grid sums, exponents (and kept norms) of the wave's blocks
   int qsum[kWaveSplits][kMaxSpan], shift[kWaveSplits][kMaxSpan];
   float n2[kWaveSplits][kMaxSpan];
@@ -1029,11 +1033,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   for (int item = lane; item < wave_rows * 8; item += 64) {
     const int row = item / 8, piece = item % 8;
     const int bl = row / (3 * count), d = (row / count) % 3, p = row % count;
-    const long cell = static_cast<long>(pair_token[p]) * B + b_begin + bl;
+    const long cell = static_cast<long>(__shfl(my_token, p)) * B + b_begin + bl;
     const uint4 v = load_global(reinterpret_cast<const uint4 *>(a.digits + (cell * 3 + d) * 128) + piece);
     *reinterpret_cast<uint4 *>(mine + ((bl * 3 + d) * a.max_pairs + p) * kDigitStride + 16 * piece) = v;
   }
-  const int my_row = min(pp, count - 1);
 #pragma unroll
   for (int si = 0; si < kWaveSplits; ++si) {
     const int s = s_begin + si;
@@ -1099,8 +1102,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
         est[up][r] = est[up][r] + parts[s][up][lane][r];
         if (kGh5) var[up][r] = var[up][r] + vparts[s][up][lane][r];
       }
-  score_four<kGh5>(a, e, pair_token[pp], pair_slot[pp], kRowTile * ct + row_in_tile, est[0], est[1],
-                   var[0], var[1], inputs);
+  score_four<kGh5>(a, e, my_token, my_slot, kRowTile * ct + row_in_tile, est[0], est[1], var[0],
+                   var[1], inputs);
 }
 
 
@@ -1120,6 +1123,11 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
 
 constexpr int kFusedWaves = 4;
 constexpr int kFusedThreads = 64 * kFusedWaves;
+// Tokens from which the fused screen runs: the per-channel-tile workgroups of
+// small_screen_kernel do a whole tile's work for each one-pair tile, so from
+// two tokens the fused screen is faster (Qwen3 layer: 13.0 against 17.2 us at
+// 2 tokens, 20.8 against 54.0 at 8; at one token 12.8 against 8.5).
+constexpr int kFusedScreenTokens = 2;
 constexpr int kStageAhead = 1;
 constexpr int kStageBuffers = kStageAhead + 1;
 
@@ -2879,11 +2887,13 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     const uint2 *trit_planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
     const uint16_t *statistics = static_cast<const uint16_t *>(weights->statistics);
     const long tiles = tile_bound(tokens, s.K, dims->experts);
-    // grouped batches: the fused screen (every split of a channel tile in one
-    // wave); smaller ones: a workgroup per channel tile whose waves share the
-    // splits. Both score in place; workgroups of tiles past the device's tile
-    // count exit at once, and one workgroup per token writes absent slots.
-    if ((stages & (1u << CFMOE_STAGE_SCREEN)) && grouped) {
+    // From kFusedScreenTokens tokens the fused screen (every split of a
+    // channel tile in one wave, four channel tiles per workgroup); a batch-1
+    // call: a workgroup per channel tile whose waves share the splits (lower
+    // latency for one pair per tile). Both score in place and give the same
+    // bits; workgroups of tiles past the device's tile count exit at once, and
+    // one workgroup per token writes absent slots.
+    if ((stages & (1u << CFMOE_STAGE_SCREEN)) && tokens >= kFusedScreenTokens) {
       FusedScreenArgs fs;
       fs.planes = trit_planes;
       fs.stats = statistics;
