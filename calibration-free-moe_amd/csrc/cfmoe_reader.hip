@@ -715,7 +715,12 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
 constexpr int kRowTile = 16;
 constexpr int kPairTile = 16;
 static_assert(kPairTile == kGroupPairs, "a screen workgroup holds one grouping tile");
-constexpr int kMaxSpan = 2;        // rotation blocks per split (H <= 2048)
+// Rotation blocks per split: the screens are compiled for a span of 2
+// (H <= 2048: the common shapes, registers and LDS sized for them) and of
+// kMaxSpan (H <= 4096, e.g. Gemma's 2816 = 22 blocks: seven splits of three
+// blocks and one of one).
+constexpr int kNarrowSpan = 2;
+constexpr int kMaxSpan = 4;
 constexpr int kDigitStride = 144;  // bytes per pair row of a digit plane (128 + pad)
 constexpr int kMaxRows = 2048;     // 2 I gate/up rows of one expert (I <= 1024)
 
@@ -949,15 +954,16 @@ __device__ __forceinline__ void consume(const StepLoads &l) {
 
 
 constexpr int kWaveSplits = (kMaxSplits + kSmallWaves - 1) / kSmallWaves;
-constexpr int kWaveBlocks = kWaveSplits * kMaxSpan;
 
-// Dynamic LDS bytes of small_screen_kernel for tiles of at most `max_pairs`.
-__host__ __device__ inline long small_screen_lds(int max_pairs) {
-  return static_cast<long>(kSmallWaves) * kWaveBlocks * 3 * max_pairs * kDigitStride;
+// Dynamic LDS bytes of small_screen_kernel<.., span> for tiles of at most
+// `max_pairs`.
+__host__ __device__ inline long small_screen_lds(int max_pairs, int span) {
+  return static_cast<long>(kSmallWaves) * kWaveSplits * span * 3 * max_pairs * kDigitStride;
 }
 
-template <bool kGh5>
+template <bool kGh5, int kSpan>
 __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScreenArgs a) {
+  constexpr int kWaveBlocks = kWaveSplits * kSpan;
   // per wave: its blocks' digit rows [block][digit][pair < max_pairs][kDigitStride]
   extern __shared__ __align__(16) int8_t small_digits[];
   __shared__ float parts[kMaxSplits][2][64][4];
@@ -995,11 +1001,11 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   // the wave's steps (split si, block j, gate/up) are loaded first
   const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64 + lane;
   const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I + row_in_tile;
-  StepLoads step[kWaveSplits][kMaxSpan][2];
+  StepLoads step[kWaveSplits][kSpan][2];
 #pragma unroll
   for (int si = 0; si < kWaveSplits; ++si)
 #pragma unroll
-    for (int j = 0; j < kMaxSpan; ++j)
+    for (int j = 0; j < kSpan; ++j)
 #pragma unroll
       for (int up = 0; up < 2; ++up) {
         const int b = min((s_begin + si) * span + j, B - 1);  // past the range: unused
@@ -1015,12 +1021,12 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   // the score's inputs (used by wave 0's live lanes) in this round trip
   const ScoreInputs inputs = load_score_inputs(a, e, my_token, my_slot, kRowTile * ct + row_in_tile);
   // the lane's pair's grid sums, exponents (and kept norms) of the wave's blocks
-  int qsum[kWaveSplits][kMaxSpan], shift[kWaveSplits][kMaxSpan];
-  float n2[kWaveSplits][kMaxSpan];
+  int qsum[kWaveSplits][kSpan], shift[kWaveSplits][kSpan];
+  float n2[kWaveSplits][kSpan];
 #pragma unroll
   for (int si = 0; si < kWaveSplits; ++si)
 #pragma unroll
-    for (int j = 0; j < kMaxSpan; ++j) {
+    for (int j = 0; j < kSpan; ++j) {
       const long cell = pair_cell + min((s_begin + si) * span + j, B - 1);
       qsum[si][j] = live_pair ? load_global(a.qsums + cell) : 0;
       shift[si][j] = live_pair ? load_global(a.qexp + cell) : 0;
@@ -1043,7 +1049,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
     if (s >= s_end) break;
     float part[2][4] = {}, vpart[2][4] = {};
 #pragma unroll
-    for (int j = 0; j < kMaxSpan; ++j) {
+    for (int j = 0; j < kSpan; ++j) {
       const int b = s * span + j;
       if (j >= span || b >= B) break;
       const int bl = b - b_begin;
@@ -1155,22 +1161,22 @@ struct FusedScreenArgs {
   int gelu, point;
 };
 
-template <bool kGh5>
+template <bool kGh5, int kSpan>
 struct FusedShared {
-  alignas(16) int8_t digits[kStageBuffers][kMaxSpan][3][kPairTile][kDigitStride];
+  alignas(16) int8_t digits[kStageBuffers][kSpan][3][kPairTile][kDigitStride];
   // the split's FP16 scales (and residual scales) of the workgroup's four
-  // gate and four up row tiles: entry 64 kind + 32 bl + 16 up + 4 w + q holds
-  // rows 4q .. 4q + 3 of wave w's row tile
-  uint2 scales[kStageBuffers][kGh5 ? 128 : 64];
-  int qsum[16][kPairTile];  // blocks (H <= 2048) x pairs
-  int shift[16][kPairTile];
-  float norm2[kGh5 ? 16 : 1][kPairTile];
+  // gate and four up row tiles: entry 32 kSpan kind + 32 bl + 16 up + 4 w + q
+  // holds rows 4q .. 4q + 3 of wave w's row tile
+  uint2 scales[kStageBuffers][(kGh5 ? 2 : 1) * kSpan * 32];
+  int qsum[kSpan * kMaxSplits][kPairTile];  // blocks x pairs
+  int shift[kSpan * kMaxSplits][kPairTile];
+  float norm2[kGh5 ? kSpan * kMaxSplits : 1][kPairTile];
   int pair_token[kPairTile], pair_slot[kPairTile];
 };
 
-template <bool kGh5>
-__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kGh5 ? 3 : 5))) void fused_screen_kernel(FusedScreenArgs a) {
-  __shared__ FusedShared<kGh5> sh;
+template <bool kGh5, int kSpan>
+__global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kSpan == kNarrowSpan ? (kGh5 ? 3 : 5) : 2))) void fused_screen_kernel(FusedScreenArgs a) {
+  __shared__ FusedShared<kGh5, kSpan> sh;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int B = a.H / 128;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
@@ -1201,9 +1207,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   // split 0's steps in flight while the tile is staged; each step's
   // successor (the next split's) is loaded into its registers as soon as the
   // step is expanded
-  uint2 step[kMaxSpan][2];
+  uint2 step[kSpan][2];
 #pragma unroll
-  for (int bl = 0; bl < kMaxSpan; ++bl)
+  for (int bl = 0; bl < kSpan; ++bl)
 #pragma unroll
     for (int up = 0; up < 2; ++up) step[bl][up] = load_step(0, bl, up);
 
@@ -1223,29 +1229,40 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     sh.pair_slot[tid] = pair % a.K;
   }
   __syncthreads();
-  // thread tid's (block, pair) entry: tid = 16 b + p (256 threads cover the
-  // 16 blocks); loaded with the first split's staging, stored after it
-  static_assert(kFusedThreads == 16 * kPairTile, "one table entry per thread");
-  const int tb = tid / kPairTile, tp = tid % kPairTile;
-  const bool table_live = tb < B && tp < count;
-  const int table_cell = table_live ? sh.pair_token[tp] * B + tb : 0;
-  const int qsum_value = load_global(a.qsums + table_cell);
-  const int shift_value = load_global(a.qexp + table_cell);
-  const float norm2_value = kGh5 ? load_global(a.norm2 + table_cell) : 0.0f;
+  // thread tid's (block, pair) entries: tid = 16 b + p, then 16 (b + 16) + p
+  // at span 4 (up to 32 blocks); loaded with the first split's staging,
+  // stored after it
+  constexpr int kTableRounds = kSpan * kMaxSplits * kPairTile / kFusedThreads;
+  static_assert(kTableRounds * kFusedThreads == kSpan * kMaxSplits * kPairTile, "table rounds");
+  const int tp = tid % kPairTile;
+  int qsum_value[kTableRounds], shift_value[kTableRounds];
+  float norm2_value[kTableRounds];
+  bool table_live[kTableRounds];
+#pragma unroll
+  for (int r = 0; r < kTableRounds; ++r) {
+    const int tb = tid / kPairTile + r * (kFusedThreads / kPairTile);
+    table_live[r] = tb < B && tp < count;
+    const int table_cell = table_live[r] ? sh.pair_token[tp] * B + tb : 0;
+    qsum_value[r] = load_global(a.qsums + table_cell);
+    shift_value[r] = load_global(a.qexp + table_cell);
+    norm2_value[r] = kGh5 ? load_global(a.norm2 + table_cell) : 0.0f;
+  }
   // staging of split s: rows (block, digit, pair) of 128 bytes, 16 bytes per
   // thread and item. Every load is unconditional and in bounds: a pair past
   // the count reads the tile's first pair (its MFMA B column feeds only that
   // pair's unused results) and a block past H or the split reads block B - 1
   // (never used)
-  constexpr int kStageRows = kMaxSpan * 3 * kPairTile;
+  constexpr int kStageRows = kSpan * 3 * kPairTile;
   constexpr int kStageItems = kStageRows * 8;  // uint4 per split
   constexpr int kStagePerThread = kStageItems / kFusedThreads;
   static_assert(kStageItems % kFusedThreads == 0, "staging items per thread");
   // Thread i also loads scale entry i (see FusedShared; threads past the
   // entries repeat entry i % entries, and a row tile past the channels reads
   // the last one)
-  constexpr int kScaleEntries = kGh5 ? 128 : 64;
-  const int sk = kGh5 ? (tid >> 6) & 1 : 0, sbl = (tid >> 5) & 1, sup = (tid >> 4) & 1;
+  constexpr int kScaleEntries = (kGh5 ? 2 : 1) * kSpan * 32;
+  static_assert(kScaleEntries <= kFusedThreads, "one scale entry per thread at most");
+  const int sentry = tid % kScaleEntries;
+  const int sk = kGh5 ? sentry / (32 * kSpan) : 0, sbl = (sentry / 32) % kSpan, sup = (tid >> 4) & 1;
   const int stile = (sup ? CT : 0) + min(group * kFusedWaves + ((tid >> 2) & 3), CT - 1);
   const int srow = (sk ? 2 * a.I : 0) + kRowTile * stile + 4 * (tid & 3);
   // each staging item's byte offset without its block term (fixed per thread)
@@ -1284,9 +1301,13 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   // (no store moves above this point: the table and staging loads are all
   // issued before the first wait)
   asm volatile("" ::: "memory");
-  sh.qsum[tb][tp] = table_live ? qsum_value : 0;
-  sh.shift[tb][tp] = table_live ? shift_value : 0;
-  if (kGh5) sh.norm2[kGh5 ? tb : 0][tp] = table_live ? norm2_value : 0.0f;
+#pragma unroll
+  for (int r = 0; r < kTableRounds; ++r) {
+    const int tb = tid / kPairTile + r * (kFusedThreads / kPairTile);
+    sh.qsum[tb][tp] = table_live[r] ? qsum_value[r] : 0;
+    sh.shift[tb][tp] = table_live[r] ? shift_value[r] : 0;
+    if (kGh5) sh.norm2[kGh5 ? tb : 0][tp] = table_live[r] ? norm2_value[r] : 0.0f;
+  }
   stage_store(0, held, held_scale);
   __syncthreads();
 
@@ -1299,7 +1320,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     // (a split's first block starts the chains from zero as an fma operand)
     float part[2][4], vpart[2][4];
 #pragma unroll
-    for (int bl = 0; bl < kMaxSpan; ++bl) {
+    for (int bl = 0; bl < kSpan; ++bl) {
       const int b = s * span + bl;
       const bool live_block = bl < span && b < B;
       const int qsum = sh.qsum[min(b, B - 1)][pp], shift = sh.shift[min(b, B - 1)][pp];
@@ -1334,7 +1355,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
       for (int up = 0; up < 2; ++up) {
         const int entry = 32 * bl + 16 * up + 4 * wave + (lane >> 4);
         const uint2 scale = sh.scales[buffer][entry];
-        const uint2 residual = kGh5 ? sh.scales[buffer][64 + entry] : make_uint2(0u, 0u);
+        const uint2 residual = kGh5 ? sh.scales[buffer][32 * kSpan + entry] : make_uint2(0u, 0u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int sum = acc[up][r];
@@ -1908,21 +1929,25 @@ struct GroupExactArgs {
   double union_row_bytes;
 };
 
-constexpr int kMaxHidden = 2048;
+constexpr int kMaxHidden = 4096;
 constexpr int kDownBuilders = 8;     // one per XCD
 constexpr int kUnionCounters = 64;  // workgroups counting the tile masks' nonzero words
-constexpr int kHiddenParts = kMaxHidden / 512;  // 16-byte parts per lane of a hidden-size row
+// 16-byte parts per lane of a hidden-size row: 4 up to H = 2048 (the common
+// shapes, 72 VGPRs in the grouped kernel), 8 up to kMaxHidden
+constexpr int kNarrowParts = 4;
+constexpr int kWideParts = kMaxHidden / 512;
+__host__ __device__ inline int hidden_parts(int H) { return H <= 512 * kNarrowParts ? kNarrowParts : kWideParts; }
 
-// Lane-ordered gate and up dots with a hidden row, each row held as
-// kHiddenParts 16-byte parts per lane (part j of lane l: h = 512 j + 8 l + i,
-// i < 8): the lane's partial sums in h order; parts past H leave them
-// untouched. Every exact row of the reader is this chain, then wave_sum_lane0.
-__device__ __forceinline__ void row_dots(const uint4 (&gw)[kHiddenParts],
-                                         const uint4 (&uw)[kHiddenParts],
-                                         const uint4 (&xw)[kHiddenParts], int H, int lane,
+// Lane-ordered gate and up dots with a hidden row, each row held as kParts
+// 16-byte parts per lane (part j of lane l: h = 512 j + 8 l + i, i < 8): the
+// lane's partial sums in h order; parts past H leave them untouched. Every
+// exact row of the reader is this chain, then wave_sum_lane0.
+template <int kParts>
+__device__ __forceinline__ void row_dots(const uint4 (&gw)[kParts], const uint4 (&uw)[kParts],
+                                         const uint4 (&xw)[kParts], int H, int lane,
                                          float &g, float &u) {
 #pragma unroll
-  for (int j = 0; j < kHiddenParts; ++j) {
+  for (int j = 0; j < kParts; ++j) {
     const bool inside = 512 * j + 8 * lane < H;
     const uint32_t gv[4] = {gw[j].x, gw[j].y, gw[j].z, gw[j].w};
     const uint32_t uv[4] = {uw[j].x, uw[j].y, uw[j].z, uw[j].w};
@@ -2108,7 +2133,8 @@ __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, i
   return -1;
 }
 
-__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(7))) void
+template <int kParts>
+__global__ __launch_bounds__(64 * kGroupExactWaves) __attribute__((amdgpu_waves_per_eu(kParts == kNarrowParts ? 7 : 4))) void
 group_exact_kernel(GroupExactArgs a) {
   const int lane = threadIdx.x & 63;
   const int block = group_exact_side_items(a, 64 * kGroupExactWaves);
@@ -2176,7 +2202,6 @@ group_exact_kernel(GroupExactArgs a) {
     const __amdgpu_buffer_rsrc_t gate_rows = buffer_resource(a.gate_up + grow, row_bytes);
     const __amdgpu_buffer_rsrc_t up_rows =
         buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
-    constexpr int kParts = kHiddenParts;
     uint4 xw[kParts];
     auto load_hidden = [&](int pp) {
       const int t = __builtin_amdgcn_readlane(token, pp);
@@ -2384,6 +2409,7 @@ struct ExactArgs {
 // hidden rows with every part in flight (buffer resources: parts past H, and
 // a padded token's hidden row, read zeros); the chain is row_dots, as in
 // group_exact_kernel.
+template <int kParts>
 __global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
   const int lane = threadIdx.x;
   const int t = blockIdx.y;
@@ -2412,9 +2438,9 @@ __global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
         buffer_resource(a.gate_up + grow + static_cast<long>(a.I) * a.H, row_bytes);
     const __amdgpu_buffer_rsrc_t hidden =
         buffer_resource(a.x + static_cast<long>(t) * a.H, active ? row_bytes : 0);
-    uint4 gw[kHiddenParts], uw[kHiddenParts], xw[kHiddenParts];
+    uint4 gw[kParts], uw[kParts], xw[kParts];
 #pragma unroll
-    for (int p = 0; p < kHiddenParts; ++p) {
+    for (int p = 0; p < kParts; ++p) {
       xw[p] = buffer_load16(hidden, offset + 1024 * p);
       gw[p] = buffer_stream16(gate_row, offset + 1024 * p);
       uw[p] = buffer_stream16(up_row, offset + 1024 * p);
@@ -2610,7 +2636,8 @@ int validate(const cfmoe_dims *d) {
   if (d->final_count < 1 || d->final_count > n) return fail(CFMOE_EINVAL, "final_count must be in [1, N]");
   if (n > kSelectThreads * kSelectKeys) return fail(CFMOE_EINVAL, "N exceeds 16384 candidates");
   if (d->experts < 1 || d->experts > kMaxExperts) return fail(CFMOE_EINVAL, "experts must be in [1, 4096]");
-  if (d->hidden > 128 * 8 * kMaxSpan) return fail(CFMOE_EINVAL, "hidden must be at most 2048");
+  if (d->hidden > 128 * 8 * kMaxSpan || d->hidden > kMaxHidden)
+    return fail(CFMOE_EINVAL, "hidden must be at most 4096");
   if (2 * d->width > kMaxRows) return fail(CFMOE_EINVAL, "width must be at most 1024");
   if (d->grouped_tokens < 0) return fail(CFMOE_EINVAL, "grouped_tokens must be >= 0");
   return 0;
@@ -2926,10 +2953,15 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       fs.gelu = gelu;
       fs.point = !gh5;
       const unsigned blocks = static_cast<unsigned>(fs.tile_items + tokens);
-      if (gh5)
-        hipLaunchKernelGGL(fused_screen_kernel<true>, dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
+      const bool narrow = s.span <= kNarrowSpan;
+      if (gh5 && narrow)
+        hipLaunchKernelGGL((fused_screen_kernel<true, kNarrowSpan>), dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
+      else if (gh5)
+        hipLaunchKernelGGL((fused_screen_kernel<true, kMaxSpan>), dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
+      else if (narrow)
+        hipLaunchKernelGGL((fused_screen_kernel<false, kNarrowSpan>), dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
       else
-        hipLaunchKernelGGL(fused_screen_kernel<false>, dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
+        hipLaunchKernelGGL((fused_screen_kernel<false, kMaxSpan>), dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
       if ((rc = check_launch("screen"))) return rc;
     } else if (stages & (1u << CFMOE_STAGE_SCREEN)) {
       SmallScreenArgs ss;
@@ -2964,11 +2996,20 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       ss.gelu = gelu;
       ss.point = !gh5;
       const unsigned blocks = static_cast<unsigned>(ss.tile_items + tokens);
-      const unsigned lds = static_cast<unsigned>(small_screen_lds(ss.max_pairs));
-      if (gh5)
-        hipLaunchKernelGGL(small_screen_kernel<true>, dim3(blocks), dim3(64 * kSmallWaves), lds, stream, ss);
+      const bool narrow = s.span <= kNarrowSpan;
+      const unsigned lds = static_cast<unsigned>(small_screen_lds(ss.max_pairs, narrow ? kNarrowSpan : kMaxSpan));
+      if (gh5 && narrow)
+        hipLaunchKernelGGL((small_screen_kernel<true, kNarrowSpan>), dim3(blocks), dim3(64 * kSmallWaves), lds,
+                           stream, ss);
+      else if (gh5)
+        hipLaunchKernelGGL((small_screen_kernel<true, kMaxSpan>), dim3(blocks), dim3(64 * kSmallWaves), lds,
+                           stream, ss);
+      else if (narrow)
+        hipLaunchKernelGGL((small_screen_kernel<false, kNarrowSpan>), dim3(blocks), dim3(64 * kSmallWaves), lds,
+                           stream, ss);
       else
-        hipLaunchKernelGGL(small_screen_kernel<false>, dim3(blocks), dim3(64 * kSmallWaves), lds, stream, ss);
+        hipLaunchKernelGGL((small_screen_kernel<false, kMaxSpan>), dim3(blocks), dim3(64 * kSmallWaves), lds,
+                           stream, ss);
       if ((rc = check_launch("screen"))) return rc;
     }
 
@@ -3061,7 +3102,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     gx.read_work = masked && (flags & CFMOE_ACCOUNT) ? workspace->read_work : nullptr;
     gx.union_row_bytes = 4.0 * s.H;
     const int counters = gx.read_work ? kUnionCounters : 0;
-    hipLaunchKernelGGL(group_exact_kernel,
+    if (hidden_parts(s.H) == kNarrowParts)
+      hipLaunchKernelGGL(group_exact_kernel<kNarrowParts>,
+                       dim3(kDownBuilders + counters + gx.tile_items + (gx.encode_items + 1) / 2 + tokens),
+                       dim3(64 * kGroupExactWaves), 0, stream, gx);
+    else
+      hipLaunchKernelGGL(group_exact_kernel<kWideParts>,
                        dim3(kDownBuilders + counters + gx.tile_items + (gx.encode_items + 1) / 2 + tokens),
                        dim3(64 * kGroupExactWaves), 0, stream, gx);
     if ((rc = check_launch("exact"))) return rc;
@@ -3084,7 +3130,12 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     ex.encode = en;
     ex.exact_blocks = s.F;
     ex.encode_items = encode_items;
-    hipLaunchKernelGGL(exact_kernel, dim3(s.F + (encode_items + 1) / 2, tokens), dim3(kWave), 0, stream, ex);
+    if (hidden_parts(s.H) == kNarrowParts)
+      hipLaunchKernelGGL(exact_kernel<kNarrowParts>, dim3(s.F + (encode_items + 1) / 2, tokens), dim3(kWave), 0,
+                         stream, ex);
+    else
+      hipLaunchKernelGGL(exact_kernel<kWideParts>, dim3(s.F + (encode_items + 1) / 2, tokens), dim3(kWave), 0,
+                         stream, ex);
     if ((rc = check_launch("exact"))) return rc;
   }
 

@@ -39,6 +39,11 @@ def test_workspace_sizes_and_contract_errors():
     bad = _ext.Dims(2000, 768, 8, 128, 32, 10, 80, 0)
     with pytest.raises(ValueError, match="multiple of 128"):
         _ext.workspace_sizes(bad, 4)
+    # hidden sizes up to 4096 (Gemma 4's 2816 among them) are accepted, wider ones refused
+    for hidden in (2816, 4096):
+        _ext.workspace_sizes(_ext.Dims(hidden, 704, 2, 4, 32, 100, 80, 0), 4)
+    with pytest.raises(ValueError, match="at most 4096"):
+        _ext.workspace_sizes(_ext.Dims(4224, 704, 2, 4, 32, 100, 80, 0), 4)
 
 
 def test_forward_rejects_null_arguments_without_touching_a_device():

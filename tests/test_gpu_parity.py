@@ -304,6 +304,36 @@ def test_benchmark_shapes_bit_exact(hidden, width, experts, top_k, retention, to
     assert report["reference_bytes"] == tokens * plan.native_read_bytes()
 
 
+@pytest.mark.parametrize(
+    "hidden,width,activation,tokens,keep,score,retention",
+    [
+        # H = 2816 (22 blocks): seven three-block screen splits and a last one of one block
+        (2816, 704, "gelu_tanh", 1, 0.625, "point", 0.125),
+        (2816, 704, "gelu_tanh", 1, 1.0, "recovery-aware", 0.2),
+        (2816, 704, "gelu_tanh", 5, 0.625, "point", 0.125),
+        (2816, 512, "silu", 16, 1.0, "recovery-aware", 0.1),
+        # H = 4096 (32 blocks): four-block splits, eight 16-byte hidden parts per lane
+        (4096, 512, "silu", 1, 0.625, "recovery-aware", 0.123),
+        (4096, 512, "silu", 20, 0.625, "point", 0.123),
+    ],
+    ids=["gemma-t1-keep80", "gemma-t1-dense-gh5", "gemma-t5", "gemma-grouped-gh5",
+         "h4096-t1-gh5", "h4096-grouped"],
+)
+def test_hidden_sizes_past_2048_bit_exact(hidden, width, activation, tokens, keep, score,
+                                          retention):
+    """Hidden sizes above 2048 (Gemma 4's 2816, and 4096) run the span-4 screens
+    and the eight-part exact rows; every stage stays bit-exact against the
+    oracle, at batch 1 (per-channel-tile screen), 5 (fused screen, per-token
+    exact rows) and from 16 (grouped rows and down order)."""
+    layer = make_layer(hidden=hidden, width=width, experts=4, top_k=2, rank=32, tokens=tokens,
+                       seed=hidden + width + tokens)
+    plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=2, retention=retention,
+                          screen_keep=keep)
+    reader = build(layer, plan, tokens, activation=activation, selection_score=score)
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+
+
 def test_graph_replay_with_changing_inputs():
     tokens = 4
     layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=60)
