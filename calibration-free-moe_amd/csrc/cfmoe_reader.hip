@@ -722,7 +722,7 @@ static_assert(kPairTile == kGroupPairs, "a screen workgroup holds one grouping t
 constexpr int kNarrowSpan = 2;
 constexpr int kMaxSpan = 4;
 constexpr int kDigitStride = 144;  // bytes per pair row of a digit plane (128 + pad)
-constexpr int kMaxRows = 2048;     // 2 I gate/up rows of one expert (I <= 1024)
+constexpr int kMaxRows = 4096;     // 2 I gate/up rows of one expert (I <= 2048)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
@@ -2477,7 +2477,7 @@ struct OutputArgs {
 };
 
 constexpr int kOutputThreads = 512;
-constexpr int kMaxEncoderTiles = 16; // ceil(I / 64) at I <= 1024
+constexpr int kMaxEncoderTiles = 16; // encoder tiles folded per batch: ceil(I / 64) at I <= 1024
 constexpr int kTileBatch = 8;        // tile partials loaded together per thread
 
 // Workgroup = `columns` outputs of one token, 512 threads (64 outputs below
@@ -2501,13 +2501,18 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   for (int item = tid; item < K * R; item += kOutputThreads) {
     const int k = item / R, r = item % R;
     const float *parts = a.encoder_parts + (static_cast<long>(t) * K + k) * a.encoder_tiles * R + r;
-    float v[kMaxEncoderTiles];
+    // batches of kMaxEncoderTiles tiles, each batch's loads issued together
+    // (one batch up to I = 1024)
+    float total = 0.0f;
+    for (int j0 = 0; j0 < a.encoder_tiles; j0 += kMaxEncoderTiles) {
+      float v[kMaxEncoderTiles];
 #pragma unroll
-    for (int j = 0; j < kMaxEncoderTiles; ++j) v[j] = j < a.encoder_tiles ? parts[j * R] : 0.0f;
-    float total = v[0];
+      for (int j = 0; j < kMaxEncoderTiles; ++j)
+        v[j] = j0 + j < a.encoder_tiles ? parts[(j0 + j) * R] : 0.0f;
 #pragma unroll
-    for (int j = 1; j < kMaxEncoderTiles; ++j)
-      if (j < a.encoder_tiles) total = total + v[j];
+      for (int j = 0; j < kMaxEncoderTiles; ++j)
+        if (j0 + j < a.encoder_tiles) total = j0 + j == 0 ? v[j] : total + v[j];
+    }
     slot_latent[k * R + r] = bfr(total);
   }
   // each slot's down tiles summed in tile order, rounded to BF16
@@ -2638,7 +2643,7 @@ int validate(const cfmoe_dims *d) {
   if (d->experts < 1 || d->experts > kMaxExperts) return fail(CFMOE_EINVAL, "experts must be in [1, 4096]");
   if (d->hidden > 128 * 8 * kMaxSpan || d->hidden > kMaxHidden)
     return fail(CFMOE_EINVAL, "hidden must be at most 4096");
-  if (2 * d->width > kMaxRows) return fail(CFMOE_EINVAL, "width must be at most 1024");
+  if (2 * d->width > kMaxRows) return fail(CFMOE_EINVAL, "width must be at most 2048");
   if (d->grouped_tokens < 0) return fail(CFMOE_EINVAL, "grouped_tokens must be >= 0");
   return 0;
 }

@@ -44,6 +44,9 @@ def test_workspace_sizes_and_contract_errors():
         _ext.workspace_sizes(_ext.Dims(hidden, 704, 2, 4, 32, 100, 80, 0), 4)
     with pytest.raises(ValueError, match="at most 4096"):
         _ext.workspace_sizes(_ext.Dims(4224, 704, 2, 4, 32, 100, 80, 0), 4)
+    _ext.workspace_sizes(_ext.Dims(2048, 2048, 8, 4, 32, 100, 80, 0), 4)
+    with pytest.raises(ValueError, match="at most 2048"):
+        _ext.workspace_sizes(_ext.Dims(2048, 2064, 2, 4, 32, 100, 80, 0), 4)
 
 
 def test_forward_rejects_null_arguments_without_touching_a_device():

@@ -315,16 +315,20 @@ def test_benchmark_shapes_bit_exact(hidden, width, experts, top_k, retention, to
         # H = 4096 (32 blocks): four-block splits, eight 16-byte hidden parts per lane
         (4096, 512, "silu", 1, 0.625, "recovery-aware", 0.123),
         (4096, 512, "silu", 20, 0.625, "point", 0.123),
+        # expert widths past 1024: Qwen3-235B's 1536 (24 encoder tiles), and 2048
+        (4096, 1536, "silu", 1, 0.625, "point", 0.123),
+        (2048, 1536, "silu", 18, 0.625, "recovery-aware", 0.123),
+        (2048, 2048, "silu", 5, 0.625, "point", 0.06),
     ],
     ids=["gemma-t1-keep80", "gemma-t1-dense-gh5", "gemma-t5", "gemma-grouped-gh5",
-         "h4096-t1-gh5", "h4096-grouped"],
+         "h4096-t1-gh5", "h4096-grouped", "qwen235b-t1", "i1536-grouped-gh5", "i2048-t5"],
 )
-def test_hidden_sizes_past_2048_bit_exact(hidden, width, activation, tokens, keep, score,
-                                          retention):
+def test_wide_layers_bit_exact(hidden, width, activation, tokens, keep, score, retention):
     """Hidden sizes above 2048 (Gemma 4's 2816, and 4096) run the span-4 screens
-    and the eight-part exact rows; every stage stays bit-exact against the
-    oracle, at batch 1 (per-channel-tile screen), 5 (fused screen, per-token
-    exact rows) and from 16 (grouped rows and down order)."""
+    and the eight-part exact rows, and widths above 1024 fold more than 16
+    encoder tiles; every stage stays bit-exact against the oracle, at batch 1
+    (per-channel-tile screen), 5 (fused screen, per-token exact rows) and from
+    16 (grouped rows and down order)."""
     layer = make_layer(hidden=hidden, width=width, experts=4, top_k=2, rank=32, tokens=tokens,
                        seed=hidden + width + tokens)
     plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=2, retention=retention,
