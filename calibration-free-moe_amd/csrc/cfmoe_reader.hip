@@ -2573,6 +2573,147 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   a.out[static_cast<long>(t) * a.H + o] = f2bf(routed + correction);
 }
 
+constexpr int kOutputItems = 8;      // (slot, output) items per thread: K x columns <= 8 x 512
+constexpr int kWideTileBatch = 4;        // tile partials of an item loaded with the other items'
+
+// The output launch from 128 tokens (512 outputs per workgroup): the same
+// arithmetic as output_kernel in two round trips, first the token's slot
+// records (into LDS), each thread's encoder tiles and its output's decoder
+// row, then the tile partials of all of the thread's (slot k, output) items
+// at once (c4: 26.7 -> 23.4 us; below 128 tokens, where a workgroup holds
+// fewer items, output_kernel's order is faster). Each
+// item sums its slot's 32-channel tile partials in tile order and rounds to
+// BF16; one thread per output then mixes the slots in order with the router
+// weights and adds the decoder correction. The per-(slot, output) values
+// live in dynamic LDS.
+__global__ __launch_bounds__(kOutputThreads) void output_wide_kernel(OutputArgs a) {
+  __shared__ float slot_latent[kMaxSlots * kMaxRank];
+  __shared__ float latent[kMaxRank];
+  __shared__ float slot_weight[kMaxSlots];
+  __shared__ int slot_first[kMaxSlots], slot_tiles[kMaxSlots];
+  extern __shared__ float slot_value[];  // [K][columns]
+  const int t = blockIdx.y, tid = threadIdx.x;
+  const int columns = a.columns;
+  const int o0 = blockIdx.x * columns;
+  const int K = a.K, R = a.R;
+  const int o = o0 + tid;
+  const bool mine = tid < columns && o < a.H;
+  // round trip 1: slot records, encoder tiles, decoder row
+  for (int k = tid; k < K; k += kOutputThreads) {
+    slot_weight[k] = a.weights[t * K + k];
+    const int first = a.down_tile_starts[t * K + k];
+    slot_first[k] = first;
+    slot_tiles[k] = min((a.counts[t * K + k] + kDownTile - 1) / kDownTile, a.max_tiles - first);
+  }
+  const bool direct_encoder = K * R <= kOutputThreads && a.encoder_tiles <= kMaxEncoderTiles;
+  float encoder_v[kMaxEncoderTiles];
+  if (direct_encoder && tid < K * R) {
+    const float *parts = a.encoder_parts + (static_cast<long>(t) * K + tid / R) * a.encoder_tiles * R + tid % R;
+#pragma unroll
+    for (int j = 0; j < kMaxEncoderTiles; ++j) encoder_v[j] = j < a.encoder_tiles ? parts[j * R] : 0.0f;
+  }
+  const bool active = is_active(a.padding, t);
+  const bool row_ahead = R > 0 && a.decoder && (R & 7) == 0 && R <= 32;
+  uint4 decoder_row[4];
+  if (row_ahead) {
+    const uint16_t *row = a.decoder + static_cast<long>(min(o, a.H - 1)) * R;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      decoder_row[q] = 8 * q < R && active ? *reinterpret_cast<const uint4 *>(row + 8 * q) : make_uint4(0, 0, 0, 0);
+  }
+  __syncthreads();
+  // round trip 2: the tile partials of the thread's items (the first
+  // kWideTileBatch tiles of each together; longer slots continue in batches)
+  const int items = K * columns;
+  float v[kOutputItems][kWideTileBatch];
+  const float *item_parts[kOutputItems];
+  int item_tiles[kOutputItems];
+#pragma unroll
+  for (int i = 0; i < kOutputItems; ++i) {
+    const int item = tid + i * kOutputThreads;
+    const int k = item < items ? item / columns : 0;
+    const int column = item < items ? item % columns : 0;
+    const int first = slot_first[k];
+    item_tiles[i] = item < items ? slot_tiles[k] : 0;
+    item_parts[i] = a.down_parts + (static_cast<long>(t) * a.max_tiles + first) * a.H + min(o0 + column, a.H - 1);
+#pragma unroll
+    for (int j = 0; j < kWideTileBatch; ++j)
+      v[i][j] = j < item_tiles[i] ? item_parts[i][static_cast<long>(j) * a.H] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < kOutputItems; ++i) {
+    const int item = tid + i * kOutputThreads;
+    if (item >= items) continue;
+    float total = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kWideTileBatch; ++j)
+      if (j < item_tiles[i]) total = j == 0 ? v[i][j] : total + v[i][j];
+    for (int j0 = kWideTileBatch; j0 < item_tiles[i]; j0 += kWideTileBatch) {
+      float w[kWideTileBatch];
+#pragma unroll
+      for (int j = 0; j < kWideTileBatch; ++j)
+        w[j] = item_parts[i][static_cast<long>(min(j0 + j, item_tiles[i] - 1)) * a.H];
+#pragma unroll
+      for (int j = 0; j < kWideTileBatch; ++j)
+        if (j0 + j < item_tiles[i]) total = total + w[j];
+    }
+    slot_value[item] = bfr(total);  // item = k * columns + column
+  }
+  // each slot's encoder tiles summed in tile order, rounded to BF16
+  if (direct_encoder) {
+    if (tid < K * R) {
+      float total = encoder_v[0];
+#pragma unroll
+      for (int j = 1; j < kMaxEncoderTiles; ++j)
+        if (j < a.encoder_tiles) total = total + encoder_v[j];
+      slot_latent[tid] = bfr(total);  // tid = k * R + r
+    }
+  } else {
+    for (int item = tid; item < K * R; item += kOutputThreads) {
+      const int k = item / R, r = item % R;
+      const float *parts = a.encoder_parts + (static_cast<long>(t) * K + k) * a.encoder_tiles * R + r;
+      float total = parts[0];
+      for (int j = 1; j < a.encoder_tiles; ++j) total = total + parts[j * R];
+      slot_latent[k * R + r] = bfr(total);
+    }
+  }
+  __syncthreads();
+  if (tid < R) {
+    float mixed = 0.0f;
+    for (int k = 0; k < K; ++k) mixed = fmaf(slot_latent[k * R + tid], slot_weight[k], mixed);
+    latent[tid] = mixed;
+    if (blockIdx.x == 0) a.latent[static_cast<long>(t) * R + tid] = mixed;
+  }
+  __syncthreads();
+  if (!mine) return;
+  float routed = 0.0f;
+  for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k * columns + tid], slot_weight[k], routed);
+  float correction = 0.0f;
+  if (R > 0 && a.decoder) {
+    float acc = 0.0f;
+    if (row_ahead) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (8 * q >= R) break;
+        const uint32_t wv[4] = {decoder_row[q].x, decoder_row[q].y, decoder_row[q].z, decoder_row[q].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = fmaf(__uint_as_float(wv[i] << 16), bfr(latent[8 * q + 2 * i]), acc);
+          acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), bfr(latent[8 * q + 2 * i + 1]), acc);
+        }
+      }
+    } else {
+      const uint16_t *row = a.decoder + static_cast<long>(o) * R;
+      for (int r = 0; r < R; ++r) {
+        const float u = active ? bf16f(row[r]) : 0.0f;
+        acc = fmaf(u, bfr(latent[r]), acc);
+      }
+    }
+    correction = bfr(acc);
+  }
+  a.out[static_cast<long>(t) * a.H + o] = f2bf(routed + correction);
+}
+
 // ---------------------------------------------------------------------------
 // host side
 
@@ -3200,9 +3341,13 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   // from 128 tokens (c3 at 128 tokens: 18.4 -> 14.6 us), 256 from the grouped
   // size, 64 below it; LDS K x columns x 4 <= 16 KB
   op.columns = !grouped ? 64 : s.K <= 8 && tokens >= 128 ? 512 : s.K <= 16 ? 256 : 64;
-  hipLaunchKernelGGL(output_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
-                     dim3(kOutputThreads), static_cast<unsigned>(s.K * op.columns * sizeof(float)),
-                     stream, op);
+  const unsigned value_lds = static_cast<unsigned>(s.K * op.columns * sizeof(float));
+  if (op.columns == 512)
+    hipLaunchKernelGGL(output_wide_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
+                       dim3(kOutputThreads), value_lds, stream, op);
+  else
+    hipLaunchKernelGGL(output_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
+                       dim3(kOutputThreads), value_lds, stream, op);
   return check_launch("output");
 }
 
