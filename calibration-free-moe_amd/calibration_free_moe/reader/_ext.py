@@ -145,6 +145,10 @@ def library() -> ctypes.CDLL:
     lib.cfmoe_pack_trit_planes.argtypes = [
         ctypes.POINTER(Dims), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p
     ]
+    lib.cfmoe_unpack_trit_planes.restype = ctypes.c_int
+    lib.cfmoe_unpack_trit_planes.argtypes = [
+        ctypes.POINTER(Dims), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p
+    ]
     lib.cfmoe_build_sketch.restype = ctypes.c_int
     lib.cfmoe_build_sketch.argtypes = [
         ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,

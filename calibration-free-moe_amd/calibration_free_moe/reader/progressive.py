@@ -460,25 +460,26 @@ class ProgressiveReader:
         self.sketch_signs = block_hadamard_signs(h, device)
         if sketch is None:
             sketch = build_sketch(gate_up, self.sketch_signs)
-        self.sketch_codes, self.sketch_statistics = sketch
+        codes, self.sketch_statistics = sketch
         if (
-            self.sketch_codes.shape != (e, sketch_storage_bytes(2 * i, h))
-            or self.sketch_codes.dtype != torch.uint8
-            or self.sketch_codes.device != device
-            or not self.sketch_codes.is_contiguous()
+            codes.shape != (e, sketch_storage_bytes(2 * i, h))
+            or codes.dtype != torch.uint8
+            or codes.device != device
+            or not codes.is_contiguous()
             or self.sketch_statistics.shape != (e, 2 * i, h // 128, 2)
             or self.sketch_statistics.dtype != torch.float16
             or self.sketch_statistics.device != device
             or self.sketch_statistics.stride() != (4 * i * (h // 128), 1, 4 * i, 2 * i)
         ):
             raise ValueError("Sketch must match the local native routed experts")
-        self.sketch_resident_bytes = (
-            self.sketch_codes.numel() + self.sketch_statistics.numel() * 2
-        )
+        self.sketch_resident_bytes = codes.numel() + self.sketch_statistics.numel() * 2
         # The screen reads the codes through a 2-bit repacking in the order of
         # its matrix-core operands, built once here (64 I H / 128 bytes per
-        # expert); the reference streams the codes themselves.
+        # expert); the reference streams the codes themselves. Only the planes
+        # stay resident: `sketch_codes` rebuilds the codes from them when read.
+        # A dense plan never screens: it keeps the codes as given.
         self.sketch_trit_planes = torch.empty(0, dtype=torch.int32, device=device)
+        self._sketch_codes: Tensor | None = codes
         if plan.final_count < plan.candidate_count:
             dims = _dims(plan, e, rank)
             self.sketch_trit_planes = torch.empty(
@@ -487,11 +488,13 @@ class ProgressiveReader:
             _ext.check(
                 _ext.library().cfmoe_pack_trit_planes(
                     ctypes.byref(dims),
-                    self.sketch_codes.data_ptr(),
+                    codes.data_ptr(),
                     self.sketch_trit_planes.data_ptr(),
                     torch.cuda.current_stream(device).cuda_stream,
                 )
             )
+            self._sketch_codes = None
+        del codes
         self.norms = down.float().square().sum(1).sqrt()
         self.native_gu = gate_up.detach()
         self.down = down.detach()
@@ -600,7 +603,7 @@ class ProgressiveReader:
         self._weights_c = _ext.WeightPointers(
             _pointer(self.native_gu),
             _pointer(self.down),
-            _pointer(self.sketch_codes),
+            _pointer(self._sketch_codes),
             _pointer(self.sketch_statistics),
             _pointer(self.norms),
             _pointer(self.recovery_geometry),
@@ -731,6 +734,31 @@ class ProgressiveReader:
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.native_gu.device).cuda_stream
+
+    @property
+    def sketch_codes(self) -> Tensor:
+        """The sketch codes [E, sketch_storage_bytes(2 I, H)] (progressive.py:3317).
+
+        Screened plans keep only the trit planes resident, so this rebuilds
+        the codes from them (one launch, a new tensor on every read); bytes
+        that carry no channel read 121, as `build_sketch` leaves them.
+        """
+        if self._sketch_codes is not None:
+            return self._sketch_codes
+        p = self.plan
+        e = self.native_gu.shape[0]
+        codes = torch.empty(
+            (e, sketch_storage_bytes(2 * p.expert_width, p.hidden_size)),
+            dtype=torch.uint8, device=self.native_gu.device,
+        )
+        dims = _dims(p, e, self.rank)
+        _ext.check(
+            _ext.library().cfmoe_unpack_trit_planes(
+                ctypes.byref(dims), self.sketch_trit_planes.data_ptr(), codes.data_ptr(),
+                self._stream(),
+            )
+        )
+        return codes
 
     @torch.no_grad()
     def prepare_input(self, hidden: Tensor, padding: Tensor | None = None) -> bool:

@@ -729,6 +729,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 struct PackArgs {
   const uint8_t *codes;
   uint2 *planes;
+  uint8_t *codes_out;  // unpack_trit_planes_kernel's output
   long storage;  // code bytes per expert
   long total;    // uint2 words: E B RT 64
   int I, B, body;
@@ -765,6 +766,48 @@ __global__ __launch_bounds__(256) void pack_trit_planes_kernel(PackArgs a) {
       word[h] |= digit << (8 * (k % 4) + 2 * (k / 4));
     }
   a.planes[index] = make_uint2(word[0], word[1]);
+}
+
+// The inverse repacking: thread per code byte of the sketch storage (body,
+// then the block-paired tail rows), five channels' digits read back from the
+// planes; bytes that carry no channel (a channel past I, the missing half of
+// an odd block count's last tail row) hold 121, five zero trits.
+__global__ __launch_bounds__(256) void unpack_trit_planes_kernel(PackArgs a) {
+  const long index = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long experts_bytes = a.total;  // E * storage
+  if (index >= experts_bytes) return;
+  const long e = index / a.storage;
+  const long at = index % a.storage;
+  const long body_bytes = static_cast<long>(a.B) * 128 * a.body;
+  int b, c, j;
+  if (at < body_bytes) {
+    b = static_cast<int>(at / (128L * a.body));
+    const long rest = at % (128L * a.body);
+    c = static_cast<int>(rest / a.body);
+    j = static_cast<int>(rest % a.body);
+  } else {
+    const long rest = at - body_bytes;
+    const int in_row = static_cast<int>(rest % 4096);
+    b = 2 * static_cast<int>(rest / 4096) + (in_row % 32) / 16;
+    c = in_row / 32;
+    j = a.body + in_row % 16;
+  }
+  const int RT = 2 * a.I / kRowTile;
+  const int gate_up = j % 2;
+  uint32_t byte = 0u;
+  for (int d = 4; d >= 0; --d) {
+    const int channel = 5 * (j / 2) + d;
+    uint32_t digit = 1u;  // a zero trit
+    if (b < a.B && channel < a.I) {
+      const int row = gate_up * a.I + channel;
+      const int lane = 16 * ((c % 64) / 16) + row % kRowTile;
+      const uint2 w = a.planes[((e * a.B + b) * RT + row / kRowTile) * 64 + lane];
+      const int k = c % 16;
+      digit = (((c / 64) ? w.y : w.x) >> (8 * (k % 4) + 2 * (k / 4))) & 3u;
+    }
+    byte = 3u * byte + digit;
+  }
+  a.codes_out[index] = static_cast<uint8_t>(byte);
 }
 
 __device__ __forceinline__ v4i expand_digits(uint32_t x) {
@@ -2973,6 +3016,28 @@ int cfmoe_pack_trit_planes(const cfmoe_dims *dims, const uint8_t *codes, uint32_
   hipLaunchKernelGGL(pack_trit_planes_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), a);
   return check_launch("pack_trit_planes");
+}
+
+int cfmoe_unpack_trit_planes(const cfmoe_dims *dims, const uint32_t *planes, uint8_t *codes,
+                             cfmoe_stream stream) {
+  if (int rc = validate(dims)) return rc;
+  if (!codes || !planes) return fail(CFMOE_EINVAL, "NULL argument");
+  if (reinterpret_cast<uintptr_t>(planes) % 8)
+    return fail(CFMOE_EINVAL, "trit_planes must be 8-byte aligned");
+  PackArgs a;
+  a.codes = nullptr;
+  a.planes = reinterpret_cast<uint2 *>(const_cast<uint32_t *>(planes));
+  a.codes_out = codes;
+  a.I = dims->width;
+  a.B = dims->hidden / 128;
+  a.storage = storage_bytes(2 * a.I, dims->hidden);
+  const int stride = code_stride(2 * a.I);
+  a.body = stride - stride % 32;
+  a.total = static_cast<long>(dims->experts) * a.storage;
+  const long blocks = (a.total + 255) / 256;
+  hipLaunchKernelGGL(unpack_trit_planes_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("unpack_trit_planes");
 }
 
 int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,

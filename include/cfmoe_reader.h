@@ -85,7 +85,8 @@ typedef struct cfmoe_dims {
 typedef struct cfmoe_weights {
   const void *gate_up;     /* bf16 [E, 2I, H] */
   const void *down;        /* bf16, physical [E, I, H] (channel-major) */
-  const uint8_t *codes;    /* [E, sketch_storage_bytes(2I, H)]; read by cfmoe_pack_trit_planes only */
+  const uint8_t *codes;    /* unused by the forward calls (may be NULL): the screen reads
+                              trit_planes, which cfmoe_pack_trit_planes builds from the codes */
   const void *statistics;  /* fp16, physical [E, H/128, 2, 2I] */
   const float *norms;      /* [E, I] down-column L2 norms */
   const float *geometry;   /* [E, I, 2] (alpha, beta) or NULL */
@@ -185,6 +186,15 @@ CFMOE_API int64_t cfmoe_trit_plane_bytes(const cfmoe_dims *dims);
  * counterpart call in the reference. */
 CFMOE_API int cfmoe_pack_trit_planes(const cfmoe_dims *dims, const uint8_t *codes,
                                      uint32_t *trit_planes, cfmoe_stream stream);
+
+/* The inverse of cfmoe_pack_trit_planes: write the sketch codes of all
+ * `experts` ([E, sketch_storage_bytes(2I, H)], the reference's layout,
+ * sketch.py:84-150) from the trit planes, 121 (five zero trits) in every byte
+ * that carries no channel. The reader keeps only the planes resident and
+ * rebuilds the codes when its `sketch_codes` attribute is read (the reference
+ * keeps the codes themselves, progressive.py:3317); no counterpart call. */
+CFMOE_API int cfmoe_unpack_trit_planes(const cfmoe_dims *dims, const uint32_t *trit_planes,
+                                       uint8_t *codes, cfmoe_stream stream);
 
 /* Build the resident ternary sketch of `experts` experts' gate/up rows
  * (bf16 [experts, 2 width, hidden], hidden a multiple of 128) on the device:

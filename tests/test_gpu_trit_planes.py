@@ -61,3 +61,35 @@ def test_trit_planes_match_unpacked_codes(hidden, width, experts):
     want = expected_words(trits)
     mismatch = np.flatnonzero(got != want)
     assert mismatch.size == 0, f"{mismatch.size} of {got.size} words differ, first at {mismatch[:5]}"
+    # the inverse repacking gives back every code byte, the bytes that carry
+    # no channel (121, five zero trits) included
+    back = torch.zeros_like(codes)
+    _ext.check(_ext.library().cfmoe_unpack_trit_planes(
+        ctypes.byref(dims), planes.data_ptr(), back.data_ptr(),
+        torch.cuda.current_stream(DEVICE).cuda_stream))
+    torch.cuda.synchronize()
+    differ = np.flatnonzero((back != codes).cpu().numpy().reshape(-1))
+    assert differ.size == 0, f"{differ.size} of {codes.numel()} code bytes differ, first at {differ[:5]}"
+
+
+def test_reader_keeps_planes_and_rebuilds_codes():
+    """A screened reader holds no copy of the codes: `sketch_codes` rebuilds
+    them from the resident planes, equal to the codes it was given."""
+    from calibration_free_moe.reader.progressive import ProgressiveReader, channel_major_down
+
+    hidden, width, experts = 512, 256, 4
+    g = torch.Generator().manual_seed(5)
+    gate_up = (torch.randn(experts, 2 * width, hidden, generator=g) * 0.02).bfloat16().to(DEVICE)
+    down = (torch.randn(experts, hidden, width, generator=g) * 0.02).bfloat16().to(DEVICE)
+    codes, statistics = build_sketch(gate_up, block_hadamard_signs(hidden, DEVICE))
+    plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=2, retention=0.123,
+                          screen_keep=0.625)
+    reader = ProgressiveReader(gate_up, channel_major_down(down), None, None, plan, 4,
+                               sketch=(codes, statistics))
+    assert reader._sketch_codes is None and reader.sketch_trit_planes.numel() > 0
+    assert torch.equal(reader.sketch_codes, codes)
+    assert reader.sketch_resident_bytes == codes.numel() + statistics.numel() * 2
+    dense = ProgressiveReader(gate_up, channel_major_down(down), None, None,
+                              compile_budget(hidden_size=hidden, expert_width=width, top_k=2,
+                                             retention=1.0), 4, sketch=(codes, statistics))
+    assert dense.sketch_codes is codes and dense.sketch_trit_planes.numel() == 0
