@@ -1034,9 +1034,15 @@ class ProgressiveReader:
             "grouped_rows": grouped_rows,
             "grouped_issued_matrix_macs": grouped_macs,
             "workspace_bytes": float(self.workspace_bytes),
-            # the exact rows use no LDS below the grouped size (one wave per
-            # kept channel; the encoder's rank-32 rows stay in registers)
-            "batch_one_completion_shared_bytes_per_cta_upper_bound": 0.0,
+            # Below the grouped size an exact workgroup is one wave per kept
+            # channel with no LDS; at rank 32 the encoder workgroups of the
+            # same launch stage two items' 64 channel values (512 B).
+            "batch_one_completion_shared_bytes_per_cta_upper_bound": float(
+                512 * (self.rank == DIRECT_RANK)
+            ),
+            # No arrival counters (kernel boundaries order the stages), and the
+            # selection's radix histograms live in LDS: these global-scratch
+            # request counts are zero here.
             "small_batch_recovery_counter_io_bytes_per_token": 0.0,
             "small_batch_recovery_counter_sector_bytes_per_token_upper_bound": 0.0,
             "small_batch_radix_scratch_io_bytes_per_token_upper_bound": 0.0,
