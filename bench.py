@@ -181,7 +181,7 @@ def stage_kernel(stage: str, tokens: int) -> str:
     launch also scores; the score stage launches nothing)."""
     if stage == "exact" and tokens >= GROUP_EXACT_TOKENS:
         return "group_exact_kernel"
-    if stage == "screen" and tokens >= GROUP_EXACT_TOKENS:
+    if stage == "screen" and tokens >= _ext.FUSED_SCREEN_TOKENS:
         return "fused_screen_kernel"
     return STAGE_KERNELS[stage]
 

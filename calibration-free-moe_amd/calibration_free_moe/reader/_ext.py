@@ -29,6 +29,10 @@ EHIP = 2
 
 STAGES = ("prepare", "screen", "score", "select", "exact", "encode", "down", "output")
 
+# Batch size from which the screen stage launches fused_screen_kernel (below
+# it, small_screen_kernel); kFusedScreenTokens in csrc/cfmoe_reader.hip.
+FUSED_SCREEN_TOKENS = 2
+
 
 class Dims(ctypes.Structure):
     _fields_ = [

@@ -35,6 +35,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "cfmoe_reader.h"
 
@@ -52,12 +53,14 @@ __device__ __forceinline__ float bf16f(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
+// (a select, not a branch: NaN keeps its payload with the quiet bit set)
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t bits = __float_as_uint(f);
-  if ((bits & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((bits >> 16) | 0x40u);
-  bits += 0x7fffu + ((bits >> 16) & 1u);
-  return static_cast<uint16_t>(bits >> 16);
+  const uint32_t bits = __float_as_uint(f);
+  const uint32_t rounded = bits + 0x7fffu + ((bits >> 16) & 1u);
+  const uint32_t quiet = bits | 0x400000u;
+  return static_cast<uint16_t>(((bits & 0x7fffffffu) > 0x7f800000u ? quiet : rounded) >> 16);
 }
+
 
 __device__ __forceinline__ float bfr(float f) { return bf16f(f2bf(f)); }
 
@@ -245,6 +248,41 @@ __device__ __forceinline__ float wave_sum_lane0(float v) {
   return (s0 + s1) + (s2 + s3);
 }
 
+// The value of lane (lane ^ kMask), kMask = 1, 2, ..., 32, without the LDS
+// crossbar where a DPP move serves: quad permutes for 1 and 2; for 4 a quad
+// reversal, then the half-row mirror (lane i reads (i ^ 7) ^ 3 = i ^ 4); for 8
+// the row rotation by 8; for 16 a swizzle (xor mask 16 inside each half);
+// for 32 a backward permute.
+template <int kMask>
+__device__ __forceinline__ float lane_xor(float v) {
+  const int bits = __float_as_int(v);
+  if (kMask == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0xb1, 0xf, 0xf, false));
+  if (kMask == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0x4e, 0xf, 0xf, false));
+  if (kMask == 4) {
+    const int reversed = __builtin_amdgcn_mov_dpp(bits, 0x1b, 0xf, 0xf, false);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(reversed, 0x141, 0xf, 0xf, false));
+  }
+  if (kMask == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(bits, 0x128, 0xf, 0xf, false));
+  if (kMask == 16) return __int_as_float(__builtin_amdgcn_ds_swizzle(bits, 0x401f));
+  return __int_as_float(__shfl_xor(bits, 32));
+}
+
+// Largest and smallest of a wave's 64 values, every lane gets them (exact in
+// any order): the DPP tree of wave_sum_lane0, then lane reads of the rows.
+template <bool kMax>
+__device__ __forceinline__ uint32_t wave_extreme(uint32_t v) {
+  auto pick = [](uint32_t x, uint32_t y) { return kMax ? max(x, y) : min(x, y); };
+  v = pick(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0xb1, 0xf, 0xf, false)));
+  v = pick(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x4e, 0xf, 0xf, false)));
+  v = pick(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x141, 0xf, 0xf, false)));
+  v = pick(v, static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(v), 0x140, 0xf, 0xf, false)));
+  const uint32_t r0 = __builtin_amdgcn_readlane(static_cast<int>(v), 0);
+  const uint32_t r1 = __builtin_amdgcn_readlane(static_cast<int>(v), 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(static_cast<int>(v), 32);
+  const uint32_t r3 = __builtin_amdgcn_readlane(static_cast<int>(v), 48);
+  return pick(pick(r0, r1), pick(r2, r3));
+}
+
 // ---------------------------------------------------------------------------
 // block-wide reductions (thread order)
 
@@ -323,6 +361,10 @@ struct PrepareArgs {
   const uint16_t *x;
   const int8_t *signs;
   const uint8_t *padding;
+  // the padding mask as a buffer source: the mask and T bytes, or (no mask)
+  // any valid pointer and 0 bytes, whose loads read zero (active)
+  const void *padding_source;
+  int padding_bytes;
   const void *router_ids;
   const void *router_weights;
   int32_t *ids;
@@ -572,12 +614,106 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   }
 }
 
+// The routing of a one-token call on one wave, in one round trip and without
+// barriers: the same lists as route_and_group. Lane k < K holds slot k's id
+// and weight; its rank among the token's ids (ties by slot) and the summed
+// weight of equal ids come from lane reads, each lane's sorted id travels to
+// its rank by a forward permute, and the runs of equal sorted ids (ascending,
+// absent slots first) are the experts' pair lists, cut into tiles of 16.
+__device__ __forceinline__ void route_single_token(const PrepareArgs &a) {
+  // (the arguments the stores and the accounting use, loaded in one batch)
+  asm volatile("" ::"s"(a.ids), "s"(a.weights), "s"(a.pair_tiles), "s"(a.group_pairs),
+               "s"(a.group_experts), "s"(a.group_starts), "s"(a.group_counts), "s"(a.group_total),
+               "s"(a.read_work), "s"(a.tile_sketch_bytes), "s"(a.tile_screen_macs),
+               "s"(a.tile_row_bytes), "s"(a.charges[0]), "s"(a.charges[1]), "s"(a.charges[2]),
+               "s"(a.charges[3]), "s"(a.charges[4]), "s"(a.charges[5]), "s"(a.charges[6]),
+               "s"(a.charges[7]), "s"(a.charges[8]), "s"(a.charges[9]), "s"(a.charges[10]),
+               "s"(a.charges[11]), "s"(a.charges[12]), "s"(a.charges[13]), "s"(a.charges[14]),
+               "s"(a.charges[15]), "s"(a.charges[16]), "s"(a.charges[17]));
+  const int lane = threadIdx.x & 63;
+  const int K = a.K;
+  const bool in = lane < K;
+  const int p = in ? lane : K - 1;
+  // the slot's id, weight and the token's padding flag in one round trip:
+  // buffer loads of every format, none behind a branch (a resource of zero
+  // bytes reads zero: no padding mask means an active token)
+  const bool ids64 = (a.flags & CFMOE_IDS_INT64) != 0, weights16 = (a.flags & CFMOE_WEIGHTS_BF16) != 0;
+  const __amdgpu_buffer_rsrc_t ids = buffer_resource(a.router_ids, K * (ids64 ? 8 : 4));
+  const __amdgpu_buffer_rsrc_t weights = buffer_resource(a.router_weights, K * (weights16 ? 2 : 4));
+  const __amdgpu_buffer_rsrc_t padding = buffer_resource(a.padding_source, a.padding_bytes);
+  const int word0 = __builtin_amdgcn_raw_buffer_load_b32(ids, (ids64 ? 8 : 4) * p, 0, 0);
+  const int word1 = __builtin_amdgcn_raw_buffer_load_b32(ids, 8 * p + 4, 0, 0);
+  const uint32_t weight_bits = __builtin_amdgcn_raw_buffer_load_b32(weights, 4 * p, 0, 0);
+  const uint32_t weight_half = __builtin_amdgcn_raw_buffer_load_b16(weights, 2 * p, 0, 0);
+  const uint32_t padded = __builtin_amdgcn_raw_buffer_load_b8(padding, 0, 0, 0);
+  asm volatile("" ::"v"(word0), "v"(word1), "v"(weight_bits), "v"(weight_half), "v"(padded));
+  // (ids outside the int32 range are absent)
+  const int raw = !ids64 ? word0 : word1 == (word0 >> 31) ? word0 : -1;
+  const float weight = weights16 ? bf16f(static_cast<uint16_t>(weight_half)) : __uint_as_float(weight_bits);
+  const bool active = __builtin_amdgcn_readfirstlane(padded) == 0;
+  const int id = (raw < 0 || raw >= a.E) ? -1 : raw;
+  int rank = 0;
+  float w = 0.0f;  // sum of the weights of equal ids in slot order
+  for (int j = 0; j < K; ++j) {
+    const int other = __builtin_amdgcn_readlane(id, j);
+    const float other_weight = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), j));
+    rank += other < id || (other == id && j < lane);
+    if (other == id) w += other_weight;
+  }
+  if (!active) w = 0.0f;
+  if (in) {
+    a.ids[rank] = id;
+    a.weights[rank] = w;
+  }
+  // lane q: the sorted id at position q (-1: absent, or a padded token)
+  int sorted = __builtin_amdgcn_ds_permute(4 * (in ? rank : lane), active ? id : -1);
+  sorted = in ? sorted : -1;
+  const bool valid = sorted >= 0;
+  const int before = __shfl(sorted, max(lane - 1, 0));
+  const uint64_t heads = __ballot(valid && (lane == 0 || before != sorted));
+  const uint64_t upto = lane == 63 ? ~0ull : (2ull << lane) - 1ull;  // lanes 0 .. lane
+  const int run_start = valid ? 63 - __builtin_clzll(heads & upto) : 0;
+  const uint64_t later = heads & ~upto;
+  const int run_end = later ? __builtin_ctzll(later) : K;
+  const int offset = lane - run_start;
+  const bool tile_start = valid && offset % kGroupPairs == 0;
+  const uint64_t starts = __ballot(tile_start);
+  const int z = __popcll(starts & upto) - 1;
+  const int at = kGroupPairs * z + offset % kGroupPairs;
+  if (in) a.pair_tiles[lane] = valid ? at : -1;
+  if (valid) a.group_pairs[at] = lane;
+  if (tile_start) {
+    a.group_experts[z] = sorted;
+    a.group_starts[z] = kGroupPairs * z;
+    a.group_counts[z] = min(kGroupPairs, run_end - lane);
+  }
+  const int total_tiles = __popcll(starts);
+  if (lane == 0) *a.group_total = total_tiles;
+  if (a.flags & CFMOE_ACCOUNT) {
+    // (uniform indices: the charges stay kernel arguments, not private memory)
+#pragma unroll
+    for (int i = 0; i < 18; ++i)
+      if (lane == i && a.charges[i] != 0.0 && active) atomicAdd(a.read_work + i, a.charges[i]);
+    const double tiles = static_cast<double>(total_tiles);
+    if (lane == 32 && a.tile_sketch_bytes != 0.0 && total_tiles > 0)
+      atomicAdd(a.read_work + 11, tiles * a.tile_sketch_bytes);
+    if (lane == 33 && a.tile_screen_macs != 0.0 && total_tiles > 0)
+      atomicAdd(a.read_work + 15, tiles * a.tile_screen_macs);
+    if (lane == 34 && a.tile_row_bytes != 0.0 && total_tiles > 0)
+      atomicAdd(a.read_work + 12, tiles * a.tile_row_bytes);
+  }
+}
+
 template <int kPrepareThreads>
 __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
   constexpr int kPrepareWaves = kPrepareThreads / 64;
   // block 0 routes and groups (the longest block, dispatched first)
   extern __shared__ __align__(16) char route_lds[];
   __shared__ int route_scratch[32];
+  if (a.route && blockIdx.x == 0 && a.T == 1) {
+    if (threadIdx.x < 64) route_single_token(a);
+    return;
+  }
   if (a.route && blockIdx.x == 0) {
     const RouteShared shared = route_layout(route_lds, a.T * a.K, a.E);
     if (a.flags & CFMOE_IDS_INT64) {
@@ -607,14 +743,19 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
   float v1 = active ? bf16f(a.x[static_cast<long>(t) * H + base + 64 + lane]) : 0.0f;
   v0 = v0 * static_cast<float>(a.signs[base + lane]);
   v1 = v1 * static_cast<float>(a.signs[base + 64 + lane]);
-#pragma unroll
-  for (int stage = 0; stage < 6; ++stage) {
-    const int bit = 1 << stage;
-    float p0 = __shfl_xor(v0, bit);
-    float p1 = __shfl_xor(v1, bit);
-    v0 = (lane & bit) ? p0 - v0 : v0 + p0;
-    v1 = (lane & bit) ? p1 - v1 : v1 + p1;
-  }
+  // butterfly stage m: (l + r, l - r) of lanes l and l ^ m
+  auto stage = [&](auto mask) {
+    constexpr int kMask = decltype(mask)::value;
+    const float p0 = lane_xor<kMask>(v0), p1 = lane_xor<kMask>(v1);
+    v0 = (lane & kMask) ? p0 - v0 : v0 + p0;
+    v1 = (lane & kMask) ? p1 - v1 : v1 + p1;
+  };
+  stage(std::integral_constant<int, 1>());
+  stage(std::integral_constant<int, 2>());
+  stage(std::integral_constant<int, 4>());
+  stage(std::integral_constant<int, 8>());
+  stage(std::integral_constant<int, 16>());
+  stage(std::integral_constant<int, 32>());
   {
     float s = v0 + v1, d = v0 - v1;
     v0 = s * 0.08838834764831845f;
@@ -624,11 +765,17 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
   const uint32_t m1 = __float_as_uint(v1) & 0x7fffffffu;
   bool kept0 = true, kept1 = true;
   if (keep < 128) {
+    // the keep-th largest magnitude by bisection on its bits; when exactly
+    // `keep` magnitudes reach the probe, it is the least of them
     uint32_t low = 0, high = 0x7fffffffu;
     while (low < high) {
       uint32_t middle = low + ((high - low + 1u) >> 1);
       int count = __popcll(__ballot(m0 >= middle)) + __popcll(__ballot(m1 >= middle));
-      if (count >= keep) low = middle; else high = middle - 1u;
+      if (count == keep) {
+        low = wave_extreme<false>(min(m0 >= middle ? m0 : ~0u, m1 >= middle ? m1 : ~0u));
+        break;
+      }
+      if (count > keep) low = middle; else high = middle - 1u;
     }
     const uint32_t cutoff = low;
     const int above = __popcll(__ballot(m0 > cutoff)) + __popcll(__ballot(m1 > cutoff));
@@ -650,22 +797,16 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
   const long cell = static_cast<long>(t) * B + b;
   float sq = lane < keep ? compact[lane] * compact[lane] : 0.0f;
   if (lane + 64 < keep) sq = fmaf(compact[lane + 64], compact[lane + 64], sq);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) sq = sq + __shfl_xor(sq, m);
-  uint32_t peak = (kept0 ? m0 : 0u);
-  peak = max(peak, kept1 ? m1 : 0u);
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1)
-    peak = max(peak, static_cast<uint32_t>(__shfl_xor(static_cast<int>(peak), m)));
+  // (the xor-butterfly sum over the lanes, levels m = 1, 2, ..., 32)
+  sq = wave_sum_lane0(sq);
+  const uint32_t peak = wave_extreme<true>(max(kept0 ? m0 : 0u, kept1 ? m1 : 0u));
   int exponent = 0;
   if (peak) frexpf(__uint_as_float(peak), &exponent);
   const int shift = peak ? 20 - exponent : 0;
   const int32_t q0 = kept0 && peak ? static_cast<int32_t>(rintf(ldexpf(v0, shift))) : 0;
   const int32_t q1 = kept1 && peak ? static_cast<int32_t>(rintf(ldexpf(v1, shift))) : 0;
   // sum of the cell's grid values (exact in any order: |q| <= 2^20, 128 values)
-  int qsum = q0 + q1;
-#pragma unroll
-  for (int m = 1; m < 64; m <<= 1) qsum += __shfl_xor(qsum, m);
+  const int qsum = wave_sum_all(q0 + q1);
   if (lane == 0) {
     a.norm2[cell] = sq;
     a.qexp[cell] = shift;
@@ -2309,6 +2450,8 @@ struct DownArgs {
   const int32_t *order;  // workgroup b's item t * max_tiles + tile (-1: none), or NULL
   float *parts;
   int H, I, K, N, F, max_tiles;
+  const void *padding_source;  // the padding mask and T bytes, or any pointer and 0 bytes
+  int padding_bytes;
 };
 
 constexpr int kDownOutputs = 8;  // outputs per down thread (H / 8 threads)
@@ -2370,6 +2513,8 @@ __device__ __forceinline__ DownTile down_tile_slot(const int32_t *counts, const 
 // are broadcast by lane reads and every thread issues the tile's 32 row loads
 // together, then the 32 activations (one per lane, broadcast the same way).
 __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
+  asm volatile("" ::"s"(a.parts), "s"(a.down), "s"(a.activations), "s"(a.next_ids), "s"(a.padding_source),
+               "s"(a.padding_bytes), "s"(a.max_tiles), "s"(a.H), "s"(a.I), "s"(a.N), "s"(a.F));
   int tile = blockIdx.x, t = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   if (a.order) {
@@ -2381,29 +2526,41 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   const DownTile d = down_tile_slot(a.counts, a.down_tile_starts, a.ids, a.starts, a.K, t, tile);
   const int k = d.k, first = d.first, count = d.count, e = d.e, start = d.start;
   if (k < 0 || tile >= a.max_tiles) return;
-  const bool local = is_active(a.padding, t) && e >= 0;
+  // the tile's channel ids and the token's padding flag in one round trip
   const int j = first + (lane & (kDownTile - 1));
   const int logical = load_global(a.next_ids + static_cast<long>(t) * a.F + min(start + j, a.F - 1));
+  const uint32_t padded =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.padding_source, a.padding_bytes), t, 0, 0);
+  asm volatile("" ::"v"(logical), "v"(padded));
+  const bool local = __builtin_amdgcn_readfirstlane(padded) == 0 && e >= 0;
   const bool valid = j < count && start + j < a.F && logical >= 0 && logical < a.N;
   // the tile's valid ids: the prefix before the first invalid one
   const uint32_t invalid = static_cast<uint32_t>(__ballot(!valid));
   const uint32_t live = invalid ? (1u << __builtin_ctz(invalid)) - 1u : 0xffffffffu;
   const int channel = valid ? logical % a.I : 0;
-  const int o = (blockIdx.z * blockDim.x + tid) * kDownOutputs;  // z: output chunk (per-token launch)
+  // z: 512-output chunk of the per-token launch's one-wave workgroups (the
+  // grouped launch has one chunk)
+  const int o = (blockIdx.z * kWave + tid) * kDownOutputs;
   const bool outputs = o < a.H;
-  const uint16_t *rows = a.down + (local ? static_cast<long>(e) * a.I * a.H : 0) + min(o, a.H - 8);
+  // the expert's rows through one buffer resource (none without a local
+  // expert: every row then reads zeros), row c at scalar offset 2 H c; rows
+  // past the live prefix read channel 0's row, which the chain never uses
+  const __amdgpu_buffer_rsrc_t rows =
+      buffer_resource(a.down + (local ? static_cast<long>(e) * a.I * a.H : 0), local ? 2 * a.I * a.H : 0);
+  const int column = 2 * min(o, a.H - kDownOutputs);
   uint4 w[kDownTile];
 #pragma unroll
   for (int jj = 0; jj < kDownTile; ++jj) {
     const int c = __builtin_amdgcn_readlane(channel, jj);
-    const bool use = outputs && local && ((live >> jj) & 1u);
-    w[jj] = load_global(use ? reinterpret_cast<const uint4 *>(rows + static_cast<long>(c) * a.H)
-                            : &kZeroVector);
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rows, column, 2 * a.H * c, 0);
+    w[jj] = make_uint4(v.x, v.y, v.z, v.w);
   }
   const bool mine = (live >> (lane & (kDownTile - 1))) & 1u;
   const uint16_t act_bits =
       load_global(mine ? a.activations + static_cast<long>(t) * a.N + logical
                        : reinterpret_cast<const uint16_t *>(&kZeroVector));
+  // (every row load is issued before the first is used)
+  asm volatile("" ::: "memory");
   const int act_lane = static_cast<int>(__float_as_uint(bf16f(act_bits)));
   if (!outputs) return;
   float acc[kDownOutputs];
@@ -2444,6 +2601,8 @@ struct ExactArgs {
   // channel is never completed)
   EncodeArgs encode;
   int exact_blocks, encode_items;
+  const void *padding_source;  // the padding mask and T bytes, or any pointer and 0 bytes
+  int padding_bytes;
 };
 
 // Workgroup = one wave = kept channel f of token t: single-wave workgroups
@@ -2462,9 +2621,12 @@ __global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
     return;
   }
   const int f = blockIdx.x;
+  asm volatile("" ::"s"(a.partial), "s"(a.activations), "s"(a.completed), "s"(a.gate_up), "s"(a.x),
+               "s"(a.H), "s"(a.I), "s"(a.N), "s"(a.gelu), "s"(a.ids), "s"(a.next_ids), "s"(a.K),
+               "s"(a.F), "s"(a.padding_source), "s"(a.padding_bytes));
   const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
-  const uint32_t padded = __builtin_amdgcn_raw_buffer_load_b8(
-      a.padding ? buffer_resource(a.padding, t + 1) : buffer_resource(a.ids, 0), t, 0, 0);
+  const uint32_t padded =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.padding_source, a.padding_bytes), t, 0, 0);
   const int logical =
       __builtin_amdgcn_readfirstlane(load_global(a.next_ids + static_cast<long>(t) * a.F + f));
   asm volatile("" ::"v"(padded));  // the flag's load stays in this round trip
@@ -2488,6 +2650,11 @@ __global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
       gw[p] = buffer_stream16(gate_row, offset + 1024 * p);
       uw[p] = buffer_stream16(up_row, offset + 1024 * p);
     }
+    // (every row part is issued before the first is used)
+#pragma unroll
+    for (int p = 0; p < kParts; ++p)
+      asm volatile("" ::"v"(gw[p].x), "v"(gw[p].y), "v"(gw[p].z), "v"(gw[p].w), "v"(uw[p].x), "v"(uw[p].y),
+                   "v"(uw[p].z), "v"(uw[p].w), "v"(xw[p].x), "v"(xw[p].y), "v"(xw[p].z), "v"(xw[p].w));
     row_dots(gw, uw, xw, a.H, lane, g, u);
     g = wave_sum_lane0(g);
     u = wave_sum_lane0(u);
@@ -2513,6 +2680,8 @@ struct OutputArgs {
   const float *weights;
   const uint16_t *decoder;
   const uint8_t *padding;
+  const void *padding_source;  // the padding mask and T bytes, or any pointer and 0 bytes
+  int padding_bytes;
   float *latent;
   uint16_t *out;
   int H, K, R, max_tiles, encoder_tiles;
@@ -2530,15 +2699,76 @@ constexpr int kTileBatch = 8;        // tile partials loaded together per thread
 // (all loads of a batch issued together) and rounds to BF16; one thread per
 // output then mixes the slots in order with the router weights and adds the
 // decoder correction. The per-(slot, output) values live in dynamic LDS.
+// The decoder correction of one output: an fma chain over r of U[o, r] and
+// bf16(latent_r) (`rounded` holds them, 16-byte aligned; a padded token's row
+// is zero), rounded to BF16. `row_words` holds U[o, :] when R is a multiple of
+// 8 and at most 32, else the row is read here.
+__device__ __forceinline__ float decoder_correction(const OutputArgs &a, const uint4 (&row_words)[4],
+                                                    bool row_ahead, bool active, int o,
+                                                    const float *rounded) {
+  const int R = a.R;
+  float acc = 0.0f;
+  if (row_ahead) {
+    float4 l[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) l[i] = reinterpret_cast<const float4 *>(rounded)[min(i, R / 4 - 1)];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (8 * q >= R) break;
+      const uint32_t wv[4] = {active ? row_words[q].x : 0u, active ? row_words[q].y : 0u,
+                              active ? row_words[q].z : 0u, active ? row_words[q].w : 0u};
+      const float lv[8] = {l[2 * q].x, l[2 * q].y, l[2 * q].z, l[2 * q].w,
+                           l[2 * q + 1].x, l[2 * q + 1].y, l[2 * q + 1].z, l[2 * q + 1].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc = fmaf(__uint_as_float(wv[i] << 16), lv[2 * i], acc);
+        acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), lv[2 * i + 1], acc);
+      }
+    }
+  } else {
+    const uint16_t *row = a.decoder + static_cast<long>(o) * R;
+    if ((R & 7) == 0) {
+      for (int q = 0; q < R; q += 8) {
+        const uint4 w = active ? *reinterpret_cast<const uint4 *>(row + q) : make_uint4(0, 0, 0, 0);
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc = fmaf(__uint_as_float(wv[i] << 16), rounded[q + 2 * i], acc);
+          acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), rounded[q + 2 * i + 1], acc);
+        }
+      }
+    } else {
+      for (int r = 0; r < R; ++r) {
+        const float u = active ? bf16f(row[r]) : 0.0f;
+        acc = fmaf(u, rounded[r], acc);
+      }
+    }
+  }
+  return bfr(acc);
+}
+
+// The decoder row of output o0 + min(tid, columns - 1), issued before any
+// other load of the launch (R a multiple of 8, at most 32).
+__device__ __forceinline__ void load_decoder_row(const OutputArgs &a, int o0, int columns,
+                                                 uint4 (&row_words)[4]) {
+  const uint16_t *row = a.decoder + static_cast<long>(min(o0 + min(static_cast<int>(threadIdx.x), columns - 1), a.H - 1)) * a.R;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    row_words[q] = 8 * q < a.R ? *reinterpret_cast<const uint4 *>(row + 8 * q) : make_uint4(0, 0, 0, 0);
+}
+
 __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   __shared__ float slot_latent[kMaxSlots * kMaxRank];
-  __shared__ float latent[kMaxRank];
+  __shared__ __align__(16) float latent[kMaxRank];  // bf16(latent_r) of the token
   __shared__ float slot_weight[kMaxSlots];
   extern __shared__ float slot_value[];  // [K][columns]
   const int t = blockIdx.y, tid = threadIdx.x;
   const int columns = a.columns;
   const int o0 = blockIdx.x * columns;
   const int K = a.K, R = a.R;
+  const bool row_ahead = R > 0 && a.decoder && (R & 7) == 0 && R <= 32;
+  uint4 row_words[4] = {};
+  if (row_ahead) load_decoder_row(a, o0, columns, row_words);
   for (int k = tid; k < K; k += kOutputThreads) slot_weight[k] = a.weights[t * K + k];
   // each slot's encoder tiles summed in tile order, rounded to BF16
   for (int item = tid; item < K * R; item += kOutputThreads) {
@@ -2582,7 +2812,7 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   if (tid < R) {
     float mixed = 0.0f;
     for (int k = 0; k < K; ++k) mixed = fmaf(slot_latent[k * R + tid], slot_weight[k], mixed);
-    latent[tid] = mixed;
+    latent[tid] = bfr(mixed);
     if (blockIdx.x == 0) a.latent[static_cast<long>(t) * R + tid] = mixed;
   }
   __syncthreads();
@@ -2590,29 +2820,117 @@ __global__ __launch_bounds__(kOutputThreads) void output_kernel(OutputArgs a) {
   if (tid >= columns || o >= a.H) return;
   float routed = 0.0f;
   for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k * columns + tid], slot_weight[k], routed);
-  float correction = 0.0f;
-  if (R > 0 && a.decoder) {
-    const bool active = is_active(a.padding, t);
-    const uint16_t *row = a.decoder + static_cast<long>(o) * R;
-    float acc = 0.0f;
-    if ((R & 7) == 0) {
-      for (int q = 0; q < R; q += 8) {
-        const uint4 w = active ? *reinterpret_cast<const uint4 *>(row + q) : make_uint4(0, 0, 0, 0);
-        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+  const float correction =
+      R > 0 && a.decoder ? decoder_correction(a, row_words, row_ahead, is_active(a.padding, t), o, latent) : 0.0f;
+  a.out[static_cast<long>(t) * a.H + o] = f2bf(routed + correction);
+}
+
+// Output below the grouped size in one round trip: every load of the launch
+// is issued before any is used, as buffer loads over the token's ranges (a
+// read past a range returns zero, so none sits behind a branch): the decoder
+// row, the padding flag, the thread's encoder tiles (item tid = k R + r), all
+// max_tiles tile partials of the workgroup's columns (kRounds per thread, into
+// LDS) and the slot records. Each item then sums its slot's tiles from LDS in
+// the order of output_kernel, with the same roundings. The host launches it
+// for K R <= 512 threads, at most kMaxEncoderTiles encoder tiles and
+// max_tiles x columns <= kRounds x 512 partials.
+constexpr int kStagedRoundsMax = 16;  // 32 KB of staged partials
+
+template <int kRounds>
+__global__ __launch_bounds__(kOutputThreads) void output_staged_kernel(OutputArgs a) {
+  __shared__ float slot_latent[kMaxSlots * kMaxRank];
+  __shared__ __align__(16) float latent[kMaxRank];  // bf16(latent_r) of the token
+  __shared__ float slot_weight[kMaxSlots];
+  __shared__ int slot_first[kMaxSlots], slot_tiles[kMaxSlots];
+  extern __shared__ float slot_value[];  // [K][columns], then the partials [max_tiles][columns]
+  const int t = blockIdx.y, tid = threadIdx.x;
+  const int columns = a.columns;
+  const int o0 = blockIdx.x * columns;
+  const int K = a.K, R = a.R;
+  const bool row_ahead = R > 0 && a.decoder && (R & 7) == 0 && R <= 32;
+  uint4 row_words[4] = {};
+  if (row_ahead) load_decoder_row(a, o0, columns, row_words);
+  const uint32_t padded =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.padding_source, a.padding_bytes), t, 0, 0);
+  // encoder tiles of item tid (tiles past the item's read another item's or zero)
+  const int item_tiles = K * a.encoder_tiles * R;
+  const __amdgpu_buffer_rsrc_t encoder =
+      buffer_resource(a.encoder_parts + static_cast<long>(t) * item_tiles, 4 * item_tiles);
+  const int encoder_item = min(tid, max(K * R - 1, 0));
+  const int encoder_base = ((encoder_item / max(R, 1)) * a.encoder_tiles * R + encoder_item % max(R, 1)) * 4;
+  float encoder_v[kMaxEncoderTiles];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc = fmaf(__uint_as_float(wv[i] << 16), bfr(latent[q + 2 * i]), acc);
-          acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), bfr(latent[q + 2 * i + 1]), acc);
-        }
-      }
-    } else {
-      for (int r = 0; r < R; ++r) {
-        const float u = active ? bf16f(row[r]) : 0.0f;
-        acc = fmaf(u, bfr(latent[r]), acc);
-      }
-    }
-    correction = bfr(acc);
+  for (int j = 0; j < kMaxEncoderTiles; ++j)
+    encoder_v[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(encoder, encoder_base + 4 * j * R, 0, 0));
+  // the staged partials: item i = tid + 512 j is (tile i / columns, column i % columns)
+  const __amdgpu_buffer_rsrc_t parts =
+      buffer_resource(a.down_parts + static_cast<long>(t) * a.max_tiles * a.H, 4 * a.max_tiles * a.H);
+  float v[kRounds];
+#pragma unroll
+  for (int j = 0; j < kRounds; ++j) {
+    const int item = tid + j * kOutputThreads;
+    v[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        parts, ((item / columns) * a.H + o0 + item % columns) * 4, 0, 0));
   }
+  // slot records of slot tid < K
+  const __amdgpu_buffer_rsrc_t weights = buffer_resource(a.weights + t * K, 4 * K);
+  const __amdgpu_buffer_rsrc_t firsts = buffer_resource(a.down_tile_starts + t * K, 4 * K);
+  const __amdgpu_buffer_rsrc_t counts = buffer_resource(a.counts + t * K, 4 * K);
+  const uint32_t record_weight = __builtin_amdgcn_raw_buffer_load_b32(weights, 4 * tid, 0, 0);
+  const int record_first = __builtin_amdgcn_raw_buffer_load_b32(firsts, 4 * tid, 0, 0);
+  const int record_count = __builtin_amdgcn_raw_buffer_load_b32(counts, 4 * tid, 0, 0);
+  static_assert(kMaxEncoderTiles == 16, "the operand list below");
+  asm volatile("" ::"v"(encoder_v[0]), "v"(encoder_v[1]), "v"(encoder_v[2]), "v"(encoder_v[3]),
+               "v"(encoder_v[4]), "v"(encoder_v[5]), "v"(encoder_v[6]), "v"(encoder_v[7]),
+               "v"(encoder_v[8]), "v"(encoder_v[9]), "v"(encoder_v[10]), "v"(encoder_v[11]),
+               "v"(encoder_v[12]), "v"(encoder_v[13]), "v"(encoder_v[14]), "v"(encoder_v[15]),
+               "v"(record_weight), "v"(record_first), "v"(record_count), "v"(padded));
+#pragma unroll
+  for (int j = 0; j < kRounds; ++j) asm volatile("" ::"v"(v[j]));
+  float *staged = slot_value + K * columns;
+  const int entries = a.max_tiles * columns;
+#pragma unroll
+  for (int j = 0; j < kRounds; ++j)
+    if (tid + j * kOutputThreads < entries) staged[tid + j * kOutputThreads] = v[j];
+  if (tid < K) {
+    slot_weight[tid] = __uint_as_float(record_weight);
+    slot_first[tid] = record_first;
+    slot_tiles[tid] = min((record_count + kDownTile - 1) / kDownTile, a.max_tiles - record_first);
+  }
+  // each slot's encoder tiles summed in tile order, rounded to BF16
+  if (tid < K * R) {
+    float total = encoder_v[0];
+#pragma unroll
+    for (int j = 1; j < kMaxEncoderTiles; ++j)
+      if (j < a.encoder_tiles) total = total + encoder_v[j];
+    slot_latent[tid] = bfr(total);
+  }
+  __syncthreads();
+  // each slot's down tiles summed in tile order, rounded to BF16
+  for (int item = tid; item < K * columns; item += kOutputThreads) {
+    const int k = item / columns, column = item % columns;
+    const int first = slot_first[k], tiles = slot_tiles[k];
+    float total = 0.0f;
+    for (int j = 0; j < tiles; ++j) {
+      const float value = staged[(first + j) * columns + column];
+      total = j == 0 ? value : total + value;
+    }
+    slot_value[item] = bfr(total);
+  }
+  __syncthreads();
+  if (tid < R) {
+    float mixed = 0.0f;
+    for (int k = 0; k < K; ++k) mixed = fmaf(slot_latent[k * R + tid], slot_weight[k], mixed);
+    latent[tid] = bfr(mixed);
+    if (blockIdx.x == 0) a.latent[static_cast<long>(t) * R + tid] = mixed;
+  }
+  __syncthreads();
+  const int o = o0 + tid;
+  if (tid >= columns || o >= a.H) return;
+  float routed = 0.0f;
+  for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k * columns + tid], slot_weight[k], routed);
+  const float correction =
+      R > 0 && a.decoder ? decoder_correction(a, row_words, row_ahead, padded == 0, o, latent) : 0.0f;
   a.out[static_cast<long>(t) * a.H + o] = f2bf(routed + correction);
 }
 
@@ -2631,7 +2949,7 @@ constexpr int kWideTileBatch = 4;        // tile partials of an item loaded with
 // live in dynamic LDS.
 __global__ __launch_bounds__(kOutputThreads) void output_wide_kernel(OutputArgs a) {
   __shared__ float slot_latent[kMaxSlots * kMaxRank];
-  __shared__ float latent[kMaxRank];
+  __shared__ __align__(16) float latent[kMaxRank];  // bf16(latent_r) of the token
   __shared__ float slot_weight[kMaxSlots];
   __shared__ int slot_first[kMaxSlots], slot_tiles[kMaxSlots];
   extern __shared__ float slot_value[];  // [K][columns]
@@ -2724,36 +3042,15 @@ __global__ __launch_bounds__(kOutputThreads) void output_wide_kernel(OutputArgs 
   if (tid < R) {
     float mixed = 0.0f;
     for (int k = 0; k < K; ++k) mixed = fmaf(slot_latent[k * R + tid], slot_weight[k], mixed);
-    latent[tid] = mixed;
+    latent[tid] = bfr(mixed);
     if (blockIdx.x == 0) a.latent[static_cast<long>(t) * R + tid] = mixed;
   }
   __syncthreads();
   if (!mine) return;
   float routed = 0.0f;
   for (int k = 0; k < K; ++k) routed = fmaf(slot_value[k * columns + tid], slot_weight[k], routed);
-  float correction = 0.0f;
-  if (R > 0 && a.decoder) {
-    float acc = 0.0f;
-    if (row_ahead) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (8 * q >= R) break;
-        const uint32_t wv[4] = {decoder_row[q].x, decoder_row[q].y, decoder_row[q].z, decoder_row[q].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          acc = fmaf(__uint_as_float(wv[i] << 16), bfr(latent[8 * q + 2 * i]), acc);
-          acc = fmaf(__uint_as_float(wv[i] & 0xffff0000u), bfr(latent[8 * q + 2 * i + 1]), acc);
-        }
-      }
-    } else {
-      const uint16_t *row = a.decoder + static_cast<long>(o) * R;
-      for (int r = 0; r < R; ++r) {
-        const float u = active ? bf16f(row[r]) : 0.0f;
-        acc = fmaf(u, bfr(latent[r]), acc);
-      }
-    }
-    correction = bfr(acc);
-  }
+  const float correction =
+      R > 0 && a.decoder ? decoder_correction(a, decoder_row, row_ahead, active, o, latent) : 0.0f;
   a.out[static_cast<long>(t) * a.H + o] = f2bf(routed + correction);
 }
 
@@ -2828,7 +3125,10 @@ int validate(const cfmoe_dims *d) {
   if (d->hidden > 128 * 8 * kMaxSpan || d->hidden > kMaxHidden)
     return fail(CFMOE_EINVAL, "hidden must be at most 4096");
   if (2 * d->width > kMaxRows) return fail(CFMOE_EINVAL, "width must be at most 2048");
-  if (d->grouped_tokens < 0) return fail(CFMOE_EINVAL, "grouped_tokens must be >= 0");
+  // a grouped call needs the fused screen, which clears the tile masks that
+  // select and the grouped exact rows share: two tokens at least
+  if (d->grouped_tokens < 0 || d->grouped_tokens == 1)
+    return fail(CFMOE_EINVAL, "grouped_tokens must be 0 (the default) or at least 2");
   return 0;
 }
 
@@ -2880,6 +3180,8 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.x = static_cast<const uint16_t *>(hidden);
   a.signs = w->signs;
   a.padding = padding;
+  a.padding_source = padding ? static_cast<const void *>(padding) : static_cast<const void *>(w->signs);
+  a.padding_bytes = padding ? tokens : 0;
   a.router_ids = router_ids;
   a.router_weights = router_weights;
   a.ids = ws->ids;
@@ -2927,7 +3229,8 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
                     route_lds_bytes(pairs, d->experts, kWidePrepareThreads / 64) <= 96 * 1024;
   const int threads = wide ? kWidePrepareThreads : kPrepareThreads;
   const int cell_blocks = (a.cells + threads / 64 - 1) / (threads / 64);
-  const long lds = route ? route_lds_bytes(pairs, d->experts, threads / 64) : 0;
+  // (a one-token call routes on one wave, without the LDS lists)
+  const long lds = route && tokens > 1 ? route_lds_bytes(pairs, d->experts, threads / 64) : 0;
   if (wide)
     hipLaunchKernelGGL(prepare_kernel<kWidePrepareThreads>, dim3(cell_blocks + 1), dim3(threads),
                        static_cast<unsigned>(lds), stream, a);
@@ -3341,6 +3644,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     ex.encode = en;
     ex.exact_blocks = s.F;
     ex.encode_items = encode_items;
+    ex.padding_source = padding ? static_cast<const void *>(padding) : static_cast<const void *>(weights->signs);
+    ex.padding_bytes = padding ? tokens : 0;
     if (hidden_parts(s.H) == kNarrowParts)
       hipLaunchKernelGGL(exact_kernel<kNarrowParts>, dim3(s.F + (encode_items + 1) / 2, tokens), dim3(kWave), 0,
                          stream, ex);
@@ -3373,6 +3678,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     dn.N = s.N;
     dn.F = s.F;
     dn.max_tiles = s.max_tiles;
+    dn.padding_source = padding ? static_cast<const void *>(padding) : static_cast<const void *>(weights->signs);
+    dn.padding_bytes = padding ? tokens : 0;
     const int down_threads = ((s.H / kDownOutputs + kWave - 1) / kWave) * kWave;
     if (grouped) {
       hipLaunchKernelGGL(down_kernel, dim3(down_blocks), dim3(down_threads), 0, stream, dn);
@@ -3395,6 +3702,8 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.weights = workspace->weights;
   op.decoder = static_cast<const uint16_t *>(weights->decoder);
   op.padding = padding;
+  op.padding_source = padding ? static_cast<const void *>(padding) : static_cast<const void *>(weights->signs);
+  op.padding_bytes = padding ? tokens : 0;
   op.latent = workspace->latent;
   op.out = static_cast<uint16_t *>(out);
   op.H = s.H;
@@ -3407,12 +3716,22 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   // size, 64 below it; LDS K x columns x 4 <= 16 KB
   op.columns = !grouped ? 64 : s.K <= 8 && tokens >= 128 ? 512 : s.K <= 16 ? 256 : 64;
   const unsigned value_lds = static_cast<unsigned>(s.K * op.columns * sizeof(float));
+  const long staged = static_cast<long>(s.max_tiles) * op.columns;  // partials per workgroup
+  const long rounds = (staged + kOutputThreads - 1) / kOutputThreads;
+  const unsigned staged_lds = value_lds + static_cast<unsigned>(staged * sizeof(float));
+  const dim3 grid((s.H + op.columns - 1) / op.columns, tokens);
+  const bool stageable = s.H % op.columns == 0 && s.K * s.R <= kOutputThreads &&
+                         s.encoder_tiles <= kMaxEncoderTiles && rounds <= kStagedRoundsMax;
   if (op.columns == 512)
-    hipLaunchKernelGGL(output_wide_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
-                       dim3(kOutputThreads), value_lds, stream, op);
+    hipLaunchKernelGGL(output_wide_kernel, grid, dim3(kOutputThreads), value_lds, stream, op);
+  else if (stageable && rounds <= 4)
+    hipLaunchKernelGGL(output_staged_kernel<4>, grid, dim3(kOutputThreads), staged_lds, stream, op);
+  else if (stageable && rounds <= 8)
+    hipLaunchKernelGGL(output_staged_kernel<8>, grid, dim3(kOutputThreads), staged_lds, stream, op);
+  else if (stageable)
+    hipLaunchKernelGGL(output_staged_kernel<16>, grid, dim3(kOutputThreads), staged_lds, stream, op);
   else
-    hipLaunchKernelGGL(output_kernel, dim3((s.H + op.columns - 1) / op.columns, tokens),
-                       dim3(kOutputThreads), value_lds, stream, op);
+    hipLaunchKernelGGL(output_kernel, grid, dim3(kOutputThreads), value_lds, stream, op);
   return check_launch("output");
 }
 

@@ -78,7 +78,8 @@ typedef struct cfmoe_dims {
   uint32_t flags;
   int32_t grouped_tokens; /* calls of at least this many tokens compute the kept
                              channels expert-major (one read of each union row
-                             per tile of <= 16 pairs); 0 = the default, 16 */
+                             per tile of <= 16 pairs); 0 = the default, 16;
+                             otherwise at least 2 (1 is refused: EINVAL) */
 } cfmoe_dims;
 
 /* Resident per-layer tensors. The reader borrows them; none is written. */

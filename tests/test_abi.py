@@ -81,3 +81,23 @@ def test_forward_rejects_misaligned_projections_without_touching_a_device():
                                None, None)
     assert status == _ext.EINVAL
     assert b"16-byte aligned" in lib.cfmoe_last_error()
+
+
+def test_forward_refuses_a_grouped_size_of_one_token():
+    """A 1-token call runs the per-token screen, which leaves the tile masks of
+    the grouped exact rows as they are; grouped_tokens = 1 is refused before
+    any device work (0 keeps the default, 2 and more are accepted)."""
+    lib = _ext.library()
+    weights = _ext.WeightPointers()
+    workspace = _ext.WorkspacePointers()
+    workspace.capacity = 1
+    for grouped, refused in ((1, True), (-3, True), (0, False), (2, False)):
+        dims = _ext.Dims(256, 64, 2, 4, 0, 16, 80, 0, grouped)
+        status = lib.cfmoe_forward(ctypes.byref(dims), ctypes.byref(weights),
+                                   ctypes.byref(workspace), None, None, None, None, None, 1,
+                                   None, None)
+        assert status == _ext.EINVAL
+        message = lib.cfmoe_last_error()
+        assert (b"grouped_tokens" in message) == refused, message
+        if not refused:
+            assert b"NULL" in message
