@@ -1084,6 +1084,22 @@ __device__ __forceinline__ void score_four(const Args &a, int e, int token, int 
       make_float4(score[0], score[1], score[2], score[3]);
 }
 
+// The projections and score of one (pair, channel).
+template <bool kGh5, class Args>
+__device__ __forceinline__ void score_one(const Args &a, int token, int slot, int c, float gate, float up,
+                                          float gate_var, float up_var, float norm, float weight,
+                                          float alpha, float beta) {
+  const long base = static_cast<long>(token) * 2 * a.N + static_cast<long>(slot) * a.I + c;
+  a.partial[base] = gate;
+  a.partial[base + a.N] = up;
+  if (kGh5) {
+    a.variances[base] = gate_var;
+    a.variances[base + a.N] = up_var;
+  }
+  a.scores[static_cast<long>(token) * a.N + static_cast<long>(slot) * a.I + c] =
+      cfm_score(gate, up, gate_var, up_var, norm, weight, alpha, beta, a.gelu != 0, a.point != 0);
+}
+
 // ---------------------------------------------------------------------------
 // Screen and score below the grouped size (progressive.py:478-1108,
 // :1111-1353). Workgroup = (16-pair tile z, channel tile ct: gate row tile
@@ -1098,7 +1114,7 @@ __device__ __forceinline__ void score_four(const Args &a, int e, int token, int 
 // the count are zero registers, not LDS reads). Workgroups from tile_items
 // on (one per token) write the zero results of padded tokens and absent slots.
 
-constexpr int kSmallWaves = 4;
+constexpr int kSmallWaves = 8;
 constexpr int kMaxSplits = 8;
 
 struct SmallScreenArgs {
@@ -1202,8 +1218,17 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
       }
   const bool live_pair = pp < count;
   const long pair_cell = static_cast<long>(my_token) * B;
-  // the score's inputs (used by wave 0's live lanes) in this round trip
-  const ScoreInputs inputs = load_score_inputs(a, e, my_token, my_slot, kRowTile * ct + row_in_tile);
+  // the score's inputs of lane l's first epilogue item (wave 0: pair l / 16,
+  // the tile's channel l % 16) in this round trip
+  const int item_row = min(lane / kRowTile, count - 1);
+  int item_pair = slots[0];
+#pragma unroll
+  for (int p = 1; p < kPairTile; ++p) item_pair = item_row == p ? slots[p] : item_pair;
+  const int item_c = kRowTile * ct + lane % kRowTile;
+  const float item_weight = load_global(a.weights + item_pair);
+  const float item_norm = load_global(a.norms + static_cast<long>(e) * a.I + item_c);
+  const float item_alpha = a.geometry ? load_global(a.geometry + (static_cast<long>(e) * a.I + item_c) * 2) : 0.0f;
+  const float item_beta = a.geometry ? load_global(a.geometry + (static_cast<long>(e) * a.I + item_c) * 2 + 1) : 0.0f;
   // the lane's pair's grid sums, exponents (and kept norms) of the wave's blocks
   int qsum[kWaveSplits][kSpan], shift[kWaveSplits][kSpan];
   float n2[kWaveSplits][kSpan];
@@ -1275,25 +1300,37 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
     }
   }
   __syncthreads();
-  if (wave != 0 || !live_pair) return;
-  float est[2][4], var[2][4] = {};
-#pragma unroll
-  for (int up = 0; up < 2; ++up)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      est[up][r] = parts[0][up][lane][r];
-      if (kGh5) var[up][r] = vparts[0][up][lane][r];
-    }
-  for (int s = 1; s < splits; ++s)
-#pragma unroll
-    for (int up = 0; up < 2; ++up)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        est[up][r] = est[up][r] + parts[s][up][lane][r];
-        if (kGh5) var[up][r] = var[up][r] + vparts[s][up][lane][r];
+  if (wave != 0) return;
+  // wave 0 sums the splits in order and scores, one (pair p, channel row)
+  // item per lane: lane p + 16 (row / 4) holds the item's partials in its
+  // register row % 4 (the MFMA result layout)
+  for (int i = lane; i < count * kRowTile; i += kWave) {
+    const int p = i / kRowTile, row = i % kRowTile;
+    const int src = p + kRowTile * (row / 4), r = row % 4;
+    float gate = parts[0][0][src][r], up = parts[0][1][src][r];
+    float gate_var = kGh5 ? vparts[0][0][src][r] : 0.0f, up_var = kGh5 ? vparts[0][1][src][r] : 0.0f;
+    for (int s = 1; s < splits; ++s) {
+      gate = gate + parts[s][0][src][r];
+      up = up + parts[s][1][src][r];
+      if (kGh5) {
+        gate_var = gate_var + vparts[s][0][src][r];
+        up_var = up_var + vparts[s][1][src][r];
       }
-  score_four<kGh5>(a, e, my_token, my_slot, kRowTile * ct + row_in_tile, est[0], est[1], var[0],
-                   var[1], inputs);
+    }
+    int pair = item_pair;
+    float weight = item_weight, norm = item_norm, alpha = item_alpha, beta = item_beta;
+    if (i >= kWave) {  // more than four pairs: this item's inputs
+      pair = slots[0];
+#pragma unroll
+      for (int q = 1; q < kPairTile; ++q) pair = p == q ? slots[q] : pair;
+      weight = a.weights[pair];
+      norm = a.norms[static_cast<long>(e) * a.I + item_c];
+      alpha = a.geometry ? a.geometry[(static_cast<long>(e) * a.I + item_c) * 2] : 0.0f;
+      beta = a.geometry ? a.geometry[(static_cast<long>(e) * a.I + item_c) * 2 + 1] : 0.0f;
+    }
+    score_one<kGh5>(a, pair / a.K, pair % a.K, item_c, gate, up, gate_var, up_var, norm, weight, alpha,
+                    beta);
+  }
 }
 
 
