@@ -250,7 +250,20 @@ def measured_traffic(kernel: str, config: str, tokens: int, layers: int) -> dict
             "summary": os.path.relpath(path, ROOT)}
 
 
-def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> tuple[float, list[float]]:
+PILOT_SECONDS = 0.5  # the plan's pilot: replays per sample for about 0.5 s
+PLAN_SAMPLES = 7     # samples whose median is reported
+
+
+def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> dict:
+    """Replay timings of a captured layer stack.
+
+    After `warmup` untimed replays: (1) exactly `steps` replays, bracketed by
+    synchronisations, give `ms_per_step` (their mean) and per-step event
+    times; (2) the measurement plan of BASELINE.md section 3 (the reference's
+    scripts/speed_block.py:379-414): a pilot of about PILOT_SECONDS sizes a
+    sample of `replays` replays, and the median of PLAN_SAMPLES such samples
+    (each bracketed by events on the graph's stream) is `ms_median`.
+    """
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
@@ -263,8 +276,27 @@ def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> tuple[fl
         end.record()
         events.append((begin, end))
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - start
-    return elapsed * 1e3 / steps, [b.elapsed_time(e) for b, e in events]
+    ms_per_step = (time.perf_counter() - start) * 1e3 / steps
+    step_ms = [b.elapsed_time(e) for b, e in events]
+    # pilot: whole replays until about PILOT_SECONDS have passed
+    pilot, began = 0, time.perf_counter()
+    while time.perf_counter() - began < PILOT_SECONDS:
+        for _ in range(8):
+            graph.replay()
+        torch.cuda.synchronize()
+        pilot += 8
+    replays = max(1, round(pilot * PILOT_SECONDS / (time.perf_counter() - began)))
+    samples = []
+    for _ in range(PLAN_SAMPLES):
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        for _ in range(replays):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        samples.append(begin.elapsed_time(end) / replays)
+    return {"ms_per_step": ms_per_step, "step_ms": step_ms, "ms_median": statistics.median(samples),
+            "samples_ms": samples, "replays_per_sample": replays}
 
 
 _WEIGHT_CACHE: dict[int, list] = {}
@@ -315,8 +347,7 @@ def shared_expert_us(name: str, stack: list, args, device) -> float | None:
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         run()
-    ms, _ = time_graph(graph, args.warmup, args.steps)
-    return ms * 1e3 / len(stack)
+    return time_graph(graph, args.warmup, args.steps)["ms_median"] * 1e3 / len(stack)
 
 
 def run_config(name: str, args, device) -> dict:
@@ -348,9 +379,11 @@ def run_config(name: str, args, device) -> dict:
     with torch.cuda.graph(graph):
         for reader, d in stack:
             reader(d["hidden"], d["ids"], d["weights"], out=d["out"])
-    ms_per_step, samples = time_graph(graph, args.warmup, args.steps)
-    us_per_layer = ms_per_step * 1e3 / layers
-    log(f"[{name}] {us_per_layer:.2f} us/layer ({ms_per_step:.3f} ms/step)")
+    timing = time_graph(graph, args.warmup, args.steps)
+    ms_per_step = timing["ms_per_step"]
+    us_per_layer = timing["ms_median"] * 1e3 / layers
+    log(f"[{name}] {us_per_layer:.2f} us/layer (median of {PLAN_SAMPLES} samples of "
+        f"{timing['replays_per_sample']} replays; {ms_per_step:.3f} ms/step over {args.steps} steps)")
     # algorithmic bytes of each layer call, from that layer's own routes and selections
     byte_rows = []
     for reader, d in stack:
@@ -396,7 +429,9 @@ def run_config(name: str, args, device) -> dict:
         "final_count": plan.final_count,
         "ms_per_step": ms_per_step,
         "us_per_layer": us_per_layer,
-        "us_per_layer_median_event": statistics.median(samples) * 1e3 / layers,
+        "us_per_layer_steps": ms_per_step * 1e3 / layers,
+        "us_per_layer_median_event": statistics.median(timing["step_ms"]) * 1e3 / layers,
+        "replays_per_sample": timing["replays_per_sample"],
         "tokens_per_s": tokens * 1e6 / (us_per_layer * layers),
         "layer_tokens_per_s": tokens * 1e6 / us_per_layer,
         "bytes_per_layer": mean_bytes,
@@ -626,6 +661,18 @@ def main() -> int:
             "retention": retention, "screen_keep": keep, "rank": 32,
             "selection_score": "point", "final_count": headline["final_count"],
         },
+        "timing": {
+            "value": f"median of {PLAN_SAMPLES} samples after the {args.warmup} warm-up replays, each "
+                     f"sample {headline['replays_per_sample']} graph replays sized by a pilot of "
+                     f"about {PILOT_SECONDS} s (BASELINE.md section 3; the reference's "
+                     "scripts/speed_block.py:379-414), divided by the layers",
+            "ms_per_step": f"mean of exactly {args.steps} replays between synchronisations",
+            "stage_us": "each stage relaunched alone (cfmoe_launch_stage) 4 times over the stack's "
+                        "layers in one HIP graph, after one full call of the last layer: every "
+                        "relaunch reads the workspace that call left (the score stage, and the "
+                        "encode stage at rank 32, launch nothing); timing only",
+        },
+        "us_per_layer_steps": round(headline["us_per_layer_steps"], 3),
         "us_per_layer_median_step": round(headline["us_per_layer_median_event"], 3),
         "tokens_per_s": round(headline["tokens_per_s"], 1),
         "achieved_gbps": round(headline["achieved_gbps"], 1),
@@ -651,7 +698,8 @@ def main() -> int:
              if key in ("name", "description", "layers", "tokens", "retention", "screen_keep",
                         "zipf", "final_count", "us_per_layer", "tokens_per_s", "achieved_gbps",
                         "layer_roofline_frac", "dominant", "dominant_gbps", "stage_us",
-                        "shared_expert_us_per_layer", "us_per_layer_median_event")}
+                        "shared_expert_us_per_layer", "us_per_layer_median_event",
+                        "us_per_layer_steps")}
             for x in extras
         ],
     }

@@ -29,6 +29,7 @@ one fixed order.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from math import ceil
 from typing import Literal
 
@@ -472,7 +473,6 @@ class ProgressiveReader:
             or self.sketch_statistics.stride() != (4 * i * (h // 128), 1, 4 * i, 2 * i)
         ):
             raise ValueError("Sketch must match the local native routed experts")
-        self.sketch_resident_bytes = codes.numel() + self.sketch_statistics.numel() * 2
         # The screen reads the codes through a 2-bit repacking in the order of
         # its matrix-core operands, built once here (64 I H / 128 bytes per
         # expert); the reference streams the codes themselves. Only the planes
@@ -495,6 +495,15 @@ class ProgressiveReader:
             )
             self._sketch_codes = None
         del codes
+        # what stays resident: the trit planes (screened plans) or the codes,
+        # plus the FP16 statistics
+        resident = (
+            self.sketch_trit_planes.numel() * 4
+            if self._sketch_codes is None
+            else self._sketch_codes.numel()
+        )
+        self.sketch_resident_bytes = resident + self.sketch_statistics.numel() * 2
+        self._rebuilt_codes: weakref.ref | None = None
         self.norms = down.float().square().sum(1).sqrt()
         self.native_gu = gate_up.detach()
         self.down = down.detach()
@@ -740,11 +749,18 @@ class ProgressiveReader:
         """The sketch codes [E, sketch_storage_bytes(2 I, H)] (progressive.py:3317).
 
         Screened plans keep only the trit planes resident, so this rebuilds
-        the codes from them (one launch, a new tensor on every read); bytes
-        that carry no channel read 121, as `build_sketch` leaves them.
+        the codes from them (one launch); bytes that carry no channel read 121,
+        as `build_sketch` leaves them. The rebuilt tensor is held by a weak
+        reference: reads while a caller still holds it (or a view of it)
+        return that same tensor, and it is freed with the caller's last
+        reference. It is a copy: editing it does not change what the screen
+        reads.
         """
         if self._sketch_codes is not None:
             return self._sketch_codes
+        held = self._rebuilt_codes() if self._rebuilt_codes is not None else None
+        if held is not None:
+            return held
         p = self.plan
         e = self.native_gu.shape[0]
         codes = torch.empty(
@@ -758,6 +774,7 @@ class ProgressiveReader:
                 self._stream(),
             )
         )
+        self._rebuilt_codes = weakref.ref(codes)
         return codes
 
     @torch.no_grad()

@@ -64,8 +64,10 @@ def test_prepare_input_is_a_no_op_for_a_dense_plan():
 
 
 def test_default_constructor_builds_its_own_sketch():
-    """sketch=None: the reader builds the codes from its device weights (one
-    HIP launch) and screens with them; the oracle reads the same codes."""
+    """sketch=None: the reader builds the codes from its device weights by the
+    torch construction, so they are exactly `build_sketch` of the host weights
+    (test_progressive_reader.py:803-805 of the reference), and screens with
+    them; the oracle reads the same codes."""
     tokens = 3
     layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens,
                        seed=105)
@@ -76,6 +78,10 @@ def test_default_constructor_builds_its_own_sketch():
         layer.encoder.to(DEVICE), layer.decoder.to(DEVICE), plan, tokens,
         selection_score="point",
     )
+    # the reference's comparison of the two builds: codes exact, statistics
+    # to atol 1e-4 / rtol 1e-3 (the device reduces in another order)
+    assert torch.equal(reader.sketch_codes.cpu(), layer.codes)
+    torch.testing.assert_close(reader.sketch_statistics.cpu(), layer.statistics, atol=1e-4, rtol=1e-3)
     out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
     assert_parity(reader, out, expected, tokens)
 

@@ -1,8 +1,9 @@
 """Device sketch construction (cfmoe_build_sketch) against the torch build.
 
-The HIP kernel builds the reference's resident sketch format (sketch.py:84-150)
-from device weights; `build_sketch` on host weights runs the torch
-construction. The rotation is the same FP32 operations in the same order, so
+The HIP kernel (`build_sketch(..., device_kernel=True)`) builds the reference's
+resident sketch format (sketch.py:84-150) from device weights; the default
+`build_sketch` runs the torch construction on any device (the default reader
+constructor uses it, test_progressive_reader.py:803-805 of the reference). The rotation is the same FP32 operations in the same order, so
 the rotated values agree bit for bit; the sums behind mean|v|, the scale and
 the residual run in a different order. The check therefore follows the
 reference's own comparison of two sketch builds (codes exact, statistics
@@ -39,7 +40,7 @@ def test_device_sketch_matches_torch_build(experts, width, hidden, rotated):
     signs = block_hadamard_signs(hidden, "cpu") if rotated else None
     want_codes, want_stats = build_sketch(weights, signs)
     got_codes, got_stats = build_sketch(
-        weights.to(DEVICE), None if signs is None else signs.to(DEVICE)
+        weights.to(DEVICE), None if signs is None else signs.to(DEVICE), device_kernel=True
     )
     torch.cuda.synchronize()
     got_codes, got_stats = got_codes.cpu(), got_stats.cpu()
@@ -63,3 +64,17 @@ def test_device_sketch_matches_torch_build(experts, width, hidden, rotated):
     clean = ~flipped
     torch.testing.assert_close(got_stats.float()[clean], want_stats.float()[clean],
                                rtol=1e-3, atol=1e-4)
+
+
+def test_default_build_on_the_device_is_the_torch_construction():
+    """Without device_kernel, device weights get the torch construction: the
+    same codes as the build on the host, and statistics to the reference's
+    tolerance (its reductions run in the device's order)."""
+    generator = torch.Generator().manual_seed(77)
+    weights = (torch.randn(3, 2 * 96, 384, generator=generator) * 0.02).to(torch.bfloat16)
+    signs = block_hadamard_signs(384, "cpu")
+    want_codes, want_stats = build_sketch(weights, signs)
+    got_codes, got_stats = build_sketch(weights.to(DEVICE), signs.to(DEVICE))
+    torch.cuda.synchronize()
+    assert torch.equal(got_codes.cpu(), want_codes)
+    torch.testing.assert_close(got_stats.cpu(), want_stats, atol=1e-4, rtol=1e-3)

@@ -87,9 +87,19 @@ def test_reader_keeps_planes_and_rebuilds_codes():
     reader = ProgressiveReader(gate_up, channel_major_down(down), None, None, plan, 4,
                                sketch=(codes, statistics))
     assert reader._sketch_codes is None and reader.sketch_trit_planes.numel() > 0
-    assert torch.equal(reader.sketch_codes, codes)
-    assert reader.sketch_resident_bytes == codes.numel() + statistics.numel() * 2
+    rebuilt = reader.sketch_codes
+    assert torch.equal(rebuilt, codes)
+    # a held rebuild is returned again (no second unpack); once released, a
+    # read rebuilds it
+    assert reader.sketch_codes is rebuilt
+    del rebuilt
+    assert torch.equal(reader.sketch_codes[1], codes[1])
+    # resident: the planes (64 I B bytes per expert) and the FP16 statistics
+    planes_bytes = experts * 64 * width * (hidden // 128)
+    assert reader.sketch_trit_planes.numel() * 4 == planes_bytes
+    assert reader.sketch_resident_bytes == planes_bytes + statistics.numel() * 2
     dense = ProgressiveReader(gate_up, channel_major_down(down), None, None,
                               compile_budget(hidden_size=hidden, expert_width=width, top_k=2,
                                              retention=1.0), 4, sketch=(codes, statistics))
     assert dense.sketch_codes is codes and dense.sketch_trit_planes.numel() == 0
+    assert dense.sketch_resident_bytes == codes.numel() + statistics.numel() * 2

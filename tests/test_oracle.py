@@ -213,7 +213,16 @@ def bf(values):
     return values.float().bfloat16().double()
 
 
-def float64_reference(layer, plan, point=True, gelu=False, padding=None, selection=None):
+def bf16_step(values):
+    """One BF16 ulp above each BF16 value's magnitude (2^(e - 8) for a value
+    m 2^e, 0.5 <= m < 1): a bound on the distance to either BF16 neighbour."""
+    mantissa, exponent = torch.frexp(values)
+    step = torch.ldexp(torch.ones_like(values), exponent - 8)
+    return torch.where(values == 0, torch.full_like(values, 2.0 ** -133), step)
+
+
+def float64_reference(layer, plan, point=True, gelu=False, padding=None, selection=None,
+                      intervals=False):
     """Independent float64 restatement of the reader (the reference test recipe,
     tests/test_progressive_reader.py:102-267: dense trit * scale projections of
     the masked rotated input, point or Gauss-Hermite scores, a stable top-F,
@@ -221,7 +230,10 @@ def float64_reference(layer, plan, point=True, gelu=False, padding=None, selecti
 
     `selection` [T, N] bool replaces its own top-F (to compare the arithmetic
     after an identical choice). Returns outputs [T, H] (BF16 values as
-    float64), the selection, projections [T, 2, N], scores and latents.
+    float64), the selection, projections [T, 2, N], scores and latents; with
+    `intervals`, also [T, 2, N] bounds of each score over the BF16 neighbours
+    of its rounded projections (and, for the Gauss-Hermite score, of the
+    rounded product it pays), the reach of a one-ulp rounding difference.
     """
     h, i, k = plan.hidden_size, plan.expert_width, plan.top_k
     n, f = plan.candidate_count, plan.final_count
@@ -230,7 +242,7 @@ def float64_reference(layer, plan, point=True, gelu=False, padding=None, selecti
         else torch.nn.functional.silu
     experts_cache = ExpertCache(layer, plan)
     dec = layer.decoder.double()
-    outs, chosen, projections, scores_all, latents = [], [], [], [], []
+    outs, chosen, projections, scores_all, latents, bounds = [], [], [], [], [], []
     for t in range(layer.hidden.shape[0]):
         active = padding is None or not bool(padding[t])
         x = layer.hidden[t].float() if active else torch.zeros(h)
@@ -244,18 +256,10 @@ def float64_reference(layer, plan, point=True, gelu=False, padding=None, selecti
         gb, ub = bf(g), bf(u)
         nrm = torch.cat([c["norms"] for c in experts])
         wt = route.repeat_interleave(i)
-        if point:
-            score = (nrm * act(gb) * ub).square() * wt.square()
-        else:
+        if not point:
             energy = xr.double().reshape(-1, 128).square().sum(-1)
             var = torch.stack([c["residual"] @ energy for c in experts])
             sg, su = var[:, :i].reshape(-1).sqrt(), var[:, i:].reshape(-1).sqrt()
-            mu = torch.zeros_like(gb)
-            second = torch.zeros_like(gb)
-            for node, mass in zip(GH_NODES, GH_WEIGHTS):
-                a = act(gb + node * sg)
-                mu += mass * a * ub
-                second += mass * a.square() * (ub.square() + su.square())
             # recovery geometry: alpha along each down column, beta across it
             alpha, beta = [], []
             for c in experts:
@@ -264,10 +268,33 @@ def float64_reference(layer, plan, point=True, gelu=False, padding=None, selecti
                 alpha.append(a_e)
                 beta.append((response.square().sum(-1) - a_e.square()).clamp_min(0).sqrt())
             alpha, beta = torch.cat(alpha), torch.cat(beta)
+
+        def score_of(gb, ub, paid_shift=0):
+            if point:
+                return (nrm * act(gb) * ub).square() * wt.square()
+            mu = torch.zeros_like(gb)
+            second = torch.zeros_like(gb)
+            for node, mass in zip(GH_NODES, GH_WEIGHTS):
+                a = act(gb + node * sg)
+                mu += mass * a * ub
+                second += mass * a.square() * (ub.square() + su.square())
             paid = bf(act(gb) * ub)
+            paid = paid + paid_shift * bf16_step(paid)
             score = nrm.square() * (second - mu.square()).clamp_min(0)
             score = score + (nrm * mu - alpha * paid).square() + (beta * paid).square()
-            score = score * wt.square()
+            return score * wt.square()
+
+        score = score_of(gb, ub)
+        if intervals:
+            # every combination of the BF16 neighbours of bf16(g), bf16(u) (and
+            # of the paid product), widened by 1e-5 for FP32 arithmetic
+            options = []
+            for dg in (-1, 0, 1):
+                for du in (-1, 0, 1):
+                    for dp in ((0,) if point else (-1, 0, 1)):
+                        options.append(score_of(gb + dg * bf16_step(gb), ub + du * bf16_step(ub), dp))
+            options = torch.stack(options)
+            bounds.append(torch.stack((options.amin(0) * (1 - 1e-5), options.amax(0) * (1 + 1e-5))))
         if selection is None:
             kept = score.argsort(descending=True, stable=True)[:f].sort().values
             mask = torch.zeros(n, dtype=torch.bool)
@@ -292,8 +319,9 @@ def float64_reference(layer, plan, point=True, gelu=False, padding=None, selecti
         projections.append(torch.stack((g, u)))
         scores_all.append(score)
         latents.append(latent)
-    return (torch.stack(outs), torch.stack(chosen), torch.stack(projections),
-            torch.stack(scores_all), torch.stack(latents))
+    results = (torch.stack(outs), torch.stack(chosen), torch.stack(projections),
+               torch.stack(scores_all), torch.stack(latents))
+    return results + (torch.stack(bounds),) if intervals else results
 
 
 def max_relative_error(got, want) -> float:
@@ -309,14 +337,23 @@ def max_relative_error(got, want) -> float:
 OUTPUT_BOUND = 1e-2
 
 
-def assert_selection_within_rounding_band(r, scores, chosen, t, plan):
-    """Selections may differ only for candidates whose float64 score lies within
-    twice the oracle's worst score error of the float64 cutoff."""
+def assert_selection_within_rounding_band(r, scores, chosen, bounds, t, plan):
+    """Selections may differ from the float64 top-F only for candidates whose
+    score can meet the cutoff's through a one-ulp BF16 rounding difference.
+
+    The band is fixed before looking at the oracle: `bounds` holds each
+    candidate's score range over the BF16 neighbours of its rounded
+    projections (float64_reference(..., intervals=True)). A flipped candidate's
+    range must reach the range of the float64 cutoff pair (the F-th and
+    (F + 1)-th scores). Returns the number of flipped candidates.
+    """
     s = scores[t]
-    cutoff = s.sort(descending=True).values[plan.final_count - 1]
-    error = (torch.from_numpy(r["scores"][t]).double() - s).abs().max()
+    low, high = bounds[t]
+    order = torch.argsort(s, descending=True, stable=True)
+    edge = order[plan.final_count - 1: plan.final_count + 1]
+    band_low, band_high = low[edge].min(), high[edge].max()
     flipped = torch.from_numpy(r["selected"][t].astype(bool)) ^ chosen[t]
-    assert bool(((s - cutoff).abs() <= 2 * error)[flipped].all())
+    assert bool((high[flipped] >= band_low).all()) and bool((low[flipped] <= band_high).all())
     assert int(r["selected"][t].sum()) == plan.final_count
     return int(flipped.sum())
 
@@ -330,8 +367,8 @@ def test_oracle_matches_float64_reference(point):
     padding = np.array([0, 0, 1, 0], np.uint8)
     r = oracle.forward(w, bits(layer.hidden), layer.ids.numpy(), layer.weights.numpy(),
                        final_count=plan.final_count, keep=80, point=point, padding=padding)
-    out, chosen, projected, scores, _ = float64_reference(layer, plan, point=point,
-                                                          padding=torch.from_numpy(padding))
+    out, chosen, projected, scores, _, bounds = float64_reference(
+        layer, plan, point=point, padding=torch.from_numpy(padding), intervals=True)
     active = padding == 0
     # projections of skipped channels (exact rows are overwritten)
     skipped = ~r["selected"].astype(bool)
@@ -342,7 +379,7 @@ def test_oracle_matches_float64_reference(point):
     torch.testing.assert_close(torch.from_numpy(r["scores"][active]).double(),
                                scores[active], rtol=0.025, atol=1e-9)
     for t in np.flatnonzero(active):
-        assert_selection_within_rounding_band(r, scores, chosen, t, plan)
+        assert_selection_within_rounding_band(r, scores, chosen, bounds, t, plan)
     got = torch.from_numpy(oracle.bf16_to_float(r["out"])).double()
     assert max_relative_error(got[active], out[active]) <= OUTPUT_BOUND
     assert not got[~active].any()
@@ -384,31 +421,40 @@ def test_latent_is_the_encoding_of_the_skipped_channels():
 
 
 BENCHMARK_SHAPES = {
-    # per-token work of C1 (OLMoE) and C3 (Qwen3-30B-A3B) at batch 1
+    # per-token work of C1 (OLMoE), C3 (Qwen3-30B-A3B) and C5 (256 experts of
+    # width 512) at the benchmark's retention and screen keep
     "c1": dict(hidden=2048, width=1024, experts=64, top_k=8),
     "c3": dict(hidden=2048, width=768, experts=128, top_k=8),
+    "c5": dict(hidden=2048, width=512, experts=256, top_k=8),
 }
+BENCHMARK_TOKENS = 8
+# Candidates whose selection differs from the float64 top-F, over the
+# BENCHMARK_TOKENS tokens of each shape: every one must lie in the rounding
+# band, and there may be at most this many (none were measured at any shape).
+MAX_FLIPS = 2
 
 
 @pytest.fixture(scope="module", params=sorted(BENCHMARK_SHAPES))
 def benchmark_case(request):
     shape = BENCHMARK_SHAPES[request.param]
-    layer = make_routed_layer(**shape, rank=32, tokens=2, seed=17)
+    layer = make_routed_layer(**shape, rank=32, tokens=BENCHMARK_TOKENS, seed=17)
     plan = compile_budget(hidden_size=shape["hidden"], expert_width=shape["width"],
                           top_k=shape["top_k"], retention=0.123, screen_keep=0.625)
     r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
-                       layer.weights.numpy(), final_count=plan.final_count, keep=80)
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80, threads=4)
     return layer, plan, r
 
 
 def test_benchmark_shapes_selection_and_output_bound(benchmark_case):
     """At the benchmark shapes: the selection equals the float64 top-F up to
-    the rounding band, and the output meets the 1e-2 bound against the float64
-    restatement with its own selection and with the oracle's."""
+    the rounding band (at most MAX_FLIPS candidates over the tokens), and the
+    output meets the 1e-2 bound against the float64 restatement with its own
+    selection and with the oracle's."""
     layer, plan, r = benchmark_case
-    out, chosen, _, scores, _ = float64_reference(layer, plan)
-    for t in range(2):
-        assert_selection_within_rounding_band(r, scores, chosen, t, plan)
+    out, chosen, _, scores, _, bounds = float64_reference(layer, plan, intervals=True)
+    flips = sum(assert_selection_within_rounding_band(r, scores, chosen, bounds, t, plan)
+                for t in range(BENCHMARK_TOKENS))
+    assert flips <= MAX_FLIPS
     got = oracle.bf16_to_float(r["out"])
     assert max_relative_error(got, out) <= OUTPUT_BOUND
     same, _, _, _, _ = float64_reference(layer, plan, selection=r["selected"])
@@ -506,6 +552,63 @@ def test_exact_rows_are_lane_ordered_dots():
         step *= 2
     assert got == np.float32(lanes[0])
     assert got == pytest.approx(float(row.double() @ x.double()), rel=1e-5, abs=1e-5)
+
+
+def bf16_round32(values) -> np.ndarray:
+    """FP32 values rounded to BF16 (nearest even), as FP32."""
+    return oracle.bf16_to_float(oracle.bf16_bits(np.asarray(values, dtype=np.float32)))
+
+
+def test_exact_activations_round_at_each_reference_point():
+    """Every kept channel's activation is bf16(bf16(silu(bf16 g)) * bf16 u)
+    (progressive.py:1541-1546) of the oracle's own exact projections, bit for
+    bit: the BF16 roundings of the gate, of silu's result and of the up
+    projection, then one FP32 product rounded to BF16. Without the rounding
+    of silu's result some of the same channels differ, so the data tells the
+    two recipes apart."""
+    layer = small_layer(tokens=3, seed=31)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.25,
+                          screen_keep=0.625)
+    r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80)
+    kept = r["selected"].astype(bool)
+    gate, up = r["partial"][:, 0][kept], r["partial"][:, 1][kept]
+    silu = np.array([oracle.activate(float(g)) for g in bf16_round32(gate)], np.float32)
+    want = oracle.bf16_bits(bf16_round32(silu) * bf16_round32(up))
+    assert np.array_equal(r["activations"][kept], want)
+    assert (oracle.bf16_bits(silu * bf16_round32(up)) != want).any()
+
+
+def test_output_is_routed_plus_the_rounded_decoder_correction():
+    """Every output is bf16(routed + bf16(sum_r U[o, r] bf16(latent_r)))
+    (progressive.py:2081-2111), with `routed` the fma chain over slots of the
+    oracle's own BF16 slot values and router weights and the correction an
+    fma chain over ranks, bit for bit. With the latent not rounded to BF16
+    before the decoder some outputs differ, so the data tells the two apart."""
+    layer = small_layer(tokens=2, seed=33)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    r = oracle.forward(cpu_weights(layer), bits(layer.hidden), layer.ids.numpy(),
+                       layer.weights.numpy(), final_count=plan.final_count, keep=80)
+    decoder = layer.decoder.float().numpy()
+    values, weights, latent = r["values"], r["weights"], r["latent"]
+    rounded_latent = bf16_round32(latent)
+    differs = False
+    for t in range(2):
+        for o in range(512):
+            routed = 0.0
+            for k in range(4):
+                routed = exact_fmaf(float(values[t, k, o]), float(weights[t, k]), routed)
+            corrections = []
+            for lat in (rounded_latent[t], latent[t]):
+                acc = 0.0
+                for rank in range(decoder.shape[1]):
+                    acc = exact_fmaf(float(decoder[o, rank]), float(lat[rank]), acc)
+                corrections.append(bf16_round32(acc))
+            want, unrounded = (oracle.bf16_bits(np.float32(routed) + c) for c in corrections)
+            assert r["out"][t, o] == want
+            differs |= bool(want != unrounded)
+    assert differs
 
 
 def assert_dense_stock_on_retained_subset(layer, plan, r):
