@@ -1245,12 +1245,17 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   // 128 bytes, eight lanes per row
   int8_t *mine = small_digits + static_cast<long>(wave) * kWaveBlocks * 3 * a.max_pairs * kDigitStride;
   const int wave_rows = max(0, min(B, s_end * span) - min(B, b_begin)) * 3 * count;
-  for (int item = lane; item < wave_rows * 8; item += 64) {
+  // (the lane read of pair p's token runs with every lane active: a lane
+  // read from an inactive lane returns zero)
+  for (int base = 0; base < wave_rows * 8; base += 64) {
+    const int item = base + lane;
     const int row = item / 8, piece = item % 8;
     const int bl = row / (3 * count), d = (row / count) % 3, p = row % count;
     const long cell = static_cast<long>(__shfl(my_token, p)) * B + b_begin + bl;
-    const uint4 v = load_global(reinterpret_cast<const uint4 *>(a.digits + (cell * 3 + d) * 128) + piece);
-    *reinterpret_cast<uint4 *>(mine + ((bl * 3 + d) * a.max_pairs + p) * kDigitStride + 16 * piece) = v;
+    if (item < wave_rows * 8) {
+      const uint4 v = load_global(reinterpret_cast<const uint4 *>(a.digits + (cell * 3 + d) * 128) + piece);
+      *reinterpret_cast<uint4 *>(mine + ((bl * 3 + d) * a.max_pairs + p) * kDigitStride + 16 * piece) = v;
+    }
   }
 #pragma unroll
   for (int si = 0; si < kWaveSplits; ++si) {
@@ -1398,7 +1403,9 @@ struct FusedShared {
 template <bool kGh5, int kSpan>
 __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(kSpan == kNarrowSpan ? (kGh5 ? 3 : 5) : 2))) void fused_screen_kernel(FusedScreenArgs a) {
   __shared__ FusedShared<kGh5, kSpan> sh;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // (the wave index through a scalar register: every wave-uniform address
+  // term below is then scalar arithmetic, not a vector instruction per lane)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int B = a.H / 128;
   if (static_cast<int>(blockIdx.x) >= a.tile_items) {
     const int t = blockIdx.x - a.tile_items;
@@ -1416,14 +1423,17 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   const int count = load_uniform(a.group_counts + z);
   const int pp = lane % 16, k0 = 16 * (lane / 16), row_in_tile = 4 * (lane / 16);
   const int span = a.span, splits = a.splits;
-  // the wave's trit planes: gate row tile cc, up row tile CT + cc (byte
-  // offsets from the expert's planes); the scales come with the staging
+  // the wave's trit planes: gate row tile cc, up row tile CT + cc (a
+  // wave-uniform row-tile base, lane l's 8 bytes at 8 l); the scales come
+  // with the staging
   const uint2 *planes = a.planes + static_cast<long>(e) * B * RT * 64;
   const uint16_t *stats = a.stats + static_cast<long>(e) * B * 4 * a.I;
   auto load_step = [&](int s, int bl, int up) {
     const int b = min(s * span + min(bl, span - 1), B - 1);  // past H: a repeat, unused
     const int rt = up ? CT + cc : cc;
-    return load_uint2_at(planes, static_cast<uint32_t>(((b * RT + rt) * 64 + lane) * 8));
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
+        buffer_resource(planes + (b * RT + rt) * 64, 64 * 8), lane * 8, 0, 0);
+    return make_uint2(v.x, v.y);
   };
   // split 0's steps in flight while the tile is staged; each step's
   // successor (the next split's) is loaded into its registers as soon as the
@@ -1477,15 +1487,20 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   constexpr int kStageItems = kStageRows * 8;  // uint4 per split
   constexpr int kStagePerThread = kStageItems / kFusedThreads;
   static_assert(kStageItems % kFusedThreads == 0, "staging items per thread");
+  // an item's block (item / 384) is wave-uniform: 384 items are six waves
+  static_assert((8 * 3 * kPairTile) % kWave == 0, "staging blocks change at wave boundaries");
   // Thread i also loads scale entry i (see FusedShared; threads past the
   // entries repeat entry i % entries, and a row tile past the channels reads
-  // the last one)
+  // the last one). Lane offsets are fixed; per split the entries come through
+  // a buffer resource over the split's blocks to the expert's last, so an
+  // entry of a block past the expert (never used) reads zeros
   constexpr int kScaleEntries = (kGh5 ? 2 : 1) * kSpan * 32;
   static_assert(kScaleEntries <= kFusedThreads, "one scale entry per thread at most");
   const int sentry = tid % kScaleEntries;
   const int sk = kGh5 ? sentry / (32 * kSpan) : 0, sbl = (sentry / 32) % kSpan, sup = (tid >> 4) & 1;
   const int stile = (sup ? CT : 0) + min(group * kFusedWaves + ((tid >> 2) & 3), CT - 1);
   const int srow = (sk ? 2 * a.I : 0) + kRowTile * stile + 4 * (tid & 3);
+  const int scale_offset = (sbl * 4 * a.I + srow) * 2;
   // each staging item's byte offset without its block term (fixed per thread)
   int stage_offset[kStagePerThread];
 #pragma unroll
@@ -1498,13 +1513,14 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   auto stage_load = [&](int s, uint4 *held, uint2 &scale) {
 #pragma unroll
     for (int j = 0; j < kStagePerThread; ++j) {
-      const int item = tid + j * kFusedThreads;
-      const int bl = item / (8 * 3 * kPairTile);
+      const int bl = (kWave * wave + j * kFusedThreads) / (8 * 3 * kPairTile);
       const int b = min(s * span + bl, B - 1);
-      held[j] = load_uint4_at(a.digits, static_cast<uint32_t>(stage_offset[j] + b * 384));
+      held[j] = buffer_load16(buffer_resource(a.digits + b * 384, (a.T * B - b) * 384), stage_offset[j]);
     }
-    const int b = min(s * span + min(sbl, span - 1), B - 1);
-    scale = load_uint2_at(stats, static_cast<uint32_t>((b * 4 * a.I + srow) * 2));
+    const int first = min(s * span, B);  // B for the prefetch past the last split: no records
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(
+        buffer_resource(stats + first * 4 * a.I, (B - first) * 8 * a.I), scale_offset, 0, 0);
+    scale = make_uint2(v.x, v.y);
   };
   // (row (bl 3 + d) 16 + p of a buffer is item / 8: one base offset per
   // thread, item j a constant past it)
@@ -1525,28 +1541,34 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
   for (int r = 0; r < kTableRounds; ++r) {
     const int tb = tid / kPairTile + r * (kFusedThreads / kPairTile);
-    sh.qsum[tb][tp] = table_live[r] ? qsum_value[r] : 0;
-    sh.shift[tb][tp] = table_live[r] ? shift_value[r] : 0;
+    // (stored negated: the block's chain starts from -qsum and scales by
+    // 2^-shift)
+    sh.qsum[tb][tp] = table_live[r] ? -qsum_value[r] : 0;
+    sh.shift[tb][tp] = table_live[r] ? -shift_value[r] : 0;
     if (kGh5) sh.norm2[kGh5 ? tb : 0][tp] = table_live[r] ? norm2_value[r] : 0.0f;
   }
   stage_store(0, held, held_scale);
   __syncthreads();
 
   float est[2][4] = {}, var[2][4] = {};
-  for (int s = 0; s < splits; ++s) {
+  // splits from ceil(B / span) on hold no block (B = 9: splits 5-7 of span
+  // 2): their zero partials are added after the loop, so every split in it
+  // has a first block below B
+  const int live_splits = (B + span - 1) / span;
+  for (int s = 0; s < live_splits; ++s) {
     const int buffer = s % kStageBuffers;
     // split s + kStageAhead's digits go to the buffer split s - 1 used, which
     // every wave finished before the last barrier
     stage_load(s + kStageAhead, held, held_scale);
-    // (a split's first block starts the chains from zero as an fma operand)
+    // (a split's first block, always below B, starts the chains from zero
+    // as an fma operand; a later block past the split or H leaves them)
     float part[2][4], vpart[2][4];
 #pragma unroll
     for (int bl = 0; bl < kSpan; ++bl) {
       const int b = s * span + bl;
-      const bool live_block = bl < span && b < B;
-      const int qsum = sh.qsum[min(b, B - 1)][pp], shift = sh.shift[min(b, B - 1)][pp];
+      const bool live_block = bl == 0 || (bl < span && b < B);
+      const int start = sh.qsum[min(b, B - 1)][pp], shift = sh.shift[min(b, B - 1)][pp];
       const float n2 = kGh5 ? sh.norm2[kGh5 ? min(b, B - 1) : 0][pp] : 0.0f;
-      const int start = -qsum;
       auto operand = [&](int h, int d) {
         return *reinterpret_cast<const v4i *>(&sh.digits[buffer][bl][d][pp][64 * h + k0]);
       };
@@ -1560,16 +1582,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         // (the successor load stays below the expansion, so it can take the
         // step's own registers: no copy round the loop waits for it)
         asm volatile("" ::"v"(a0[up]), "v"(a1[up]) : "memory");
-        step[bl][up] = load_step(s + 1 < splits ? s + 1 : s, bl, up);
+        step[bl][up] = load_step(s + 1 < live_splits ? s + 1 : s, bl, up);
       }
-      if (!live_block) {
-        if (bl == 0)
-#pragma unroll
-          for (int up = 0; up < 2; ++up)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) part[up][r] = vpart[up][r] = 0.0f;
-        continue;
-      }
+      if (!live_block) continue;
       v4i acc[2];
       digit_dots(a0, a1, start, operand, acc);
 #pragma unroll
@@ -1580,7 +1595,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int sum = acc[up][r];
-          const float dot = ldexpf(static_cast<float>(sum), -shift);
+          const float dot = ldexpf(static_cast<float>(sum), shift);
           const uint32_t sw = r < 2 ? scale.x : scale.y;
           part[up][r] = fmaf(dot, half_at(sw, r & 1), bl == 0 ? 0.0f : part[up][r]);
           if (kGh5) {
@@ -1597,11 +1612,19 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
         est[up][r] = s == 0 ? part[up][r] : est[up][r] + part[up][r];
         if (kGh5) var[up][r] = s == 0 ? vpart[up][r] : var[up][r] + vpart[up][r];
       }
-    if (s + 1 < splits) {
+    if (s + 1 < live_splits) {
       stage_store((s + kStageAhead) % kStageBuffers, held, held_scale);
       __syncthreads();
     }
   }
+  for (int s = live_splits; s < splits; ++s)
+#pragma unroll
+    for (int up = 0; up < 2; ++up)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        est[up][r] = est[up][r] + 0.0f;
+        if (kGh5) var[up][r] = var[up][r] + 0.0f;
+      }
   // ---- score epilogue: lane (pair pp, channels c .. c + 3)
   if (!working) return;
   if (a.tile_masks && lane < kRowTile)
@@ -2599,7 +2622,8 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
   // (every row load is issued before the first is used)
   asm volatile("" ::: "memory");
   const int act_lane = static_cast<int>(__float_as_uint(bf16f(act_bits)));
-  if (!outputs) return;
+  // (every lane stays active through the chain: its lane reads fetch
+  // activations from lanes whose outputs may lie past H)
   float acc[kDownOutputs];
 #pragma unroll
   for (int i = 0; i < kDownOutputs; ++i) acc[i] = 0.0f;
@@ -2614,6 +2638,7 @@ __global__ __launch_bounds__(512) void down_kernel(DownArgs a) {
       acc[2 * i + 1] = fmaf(__uint_as_float(wv[i] & 0xffff0000u), act, acc[2 * i + 1]);
     }
   }
+  if (!outputs) return;
   float *out = a.parts + (static_cast<long>(t) * a.max_tiles + tile) * a.H + o;
   *reinterpret_cast<float4 *>(out) = make_float4(acc[0], acc[1], acc[2], acc[3]);
   *reinterpret_cast<float4 *>(out + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);

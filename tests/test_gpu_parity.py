@@ -338,6 +338,32 @@ def test_wide_layers_bit_exact(hidden, width, activation, tokens, keep, score, r
     assert_parity(reader, out, expected, tokens)
 
 
+@pytest.mark.parametrize(
+    "hidden,width,tokens,score",
+    [
+        # B = 9 blocks: eight splits of two blocks, the last three hold none
+        (1152, 256, 1, "point"),
+        (1152, 256, 5, "point"),
+        (1152, 256, 17, "recovery-aware"),
+        # B = 18: span 3 (the wide screens), splits 6 and 7 hold none
+        (2304, 512, 1, "recovery-aware"),
+        (2304, 512, 20, "point"),
+    ],
+    ids=["h1152-t1", "h1152-t5", "h1152-grouped-gh5", "h2304-t1-gh5", "h2304-grouped"],
+)
+def test_screen_splits_past_the_blocks_bit_exact(hidden, width, tokens, score):
+    """With B = 9 or 18 blocks the eight screen splits of ceil(B / 8) blocks
+    end before the last split: the empty splits add a zero partial (the
+    oracle's estimate + 0.0), in every screen kernel."""
+    layer = make_layer(hidden=hidden, width=width, experts=6, top_k=2, rank=32, tokens=tokens,
+                       seed=hidden + tokens)
+    plan = compile_budget(hidden_size=hidden, expert_width=width, top_k=2, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score=score)
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights)
+    assert_parity(reader, out, expected, tokens)
+
+
 def test_graph_replay_with_changing_inputs():
     tokens = 4
     layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=60)
