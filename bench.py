@@ -254,15 +254,18 @@ PILOT_SECONDS = 0.5  # the plan's pilot: replays per sample for about 0.5 s
 PLAN_SAMPLES = 7     # samples whose median is reported
 
 
-def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> dict:
+def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int,
+               sample_seconds: float = PILOT_SECONDS) -> dict:
     """Replay timings of a captured layer stack.
 
     After `warmup` untimed replays: (1) exactly `steps` replays, bracketed by
     synchronisations, give `ms_per_step` (their mean) and per-step event
     times; (2) the measurement plan of BASELINE.md section 3 (the reference's
-    scripts/speed_block.py:379-414): a pilot of about PILOT_SECONDS sizes a
-    sample of `replays` replays, and the median of PLAN_SAMPLES such samples
-    (each bracketed by events on the graph's stream) is `ms_median`.
+    scripts/speed_block.py:379-414): a pilot of about `sample_seconds`
+    (PILOT_SECONDS by default) sizes a sample of `replays` replays, and the
+    median of PLAN_SAMPLES such samples (each bracketed by events on the
+    graph's stream) is `ms_median`. Profiler runs pass a shorter sample, so the
+    trace holds fewer dispatch records.
     """
     for _ in range(warmup):
         graph.replay()
@@ -278,14 +281,14 @@ def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int) -> dict:
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - start) * 1e3 / steps
     step_ms = [b.elapsed_time(e) for b, e in events]
-    # pilot: whole replays until about PILOT_SECONDS have passed
+    # pilot: whole replays until about sample_seconds have passed
     pilot, began = 0, time.perf_counter()
-    while time.perf_counter() - began < PILOT_SECONDS:
+    while time.perf_counter() - began < sample_seconds:
         for _ in range(8):
             graph.replay()
         torch.cuda.synchronize()
         pilot += 8
-    replays = max(1, round(pilot * PILOT_SECONDS / (time.perf_counter() - began)))
+    replays = max(1, round(pilot * sample_seconds / (time.perf_counter() - began)))
     samples = []
     for _ in range(PLAN_SAMPLES):
         begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -347,7 +350,7 @@ def shared_expert_us(name: str, stack: list, args, device) -> float | None:
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         run()
-    return time_graph(graph, args.warmup, args.steps)["ms_median"] * 1e3 / len(stack)
+    return time_graph(graph, args.warmup, args.steps, args.sample_seconds)["ms_median"] * 1e3 / len(stack)
 
 
 def run_config(name: str, args, device) -> dict:
@@ -379,7 +382,7 @@ def run_config(name: str, args, device) -> dict:
     with torch.cuda.graph(graph):
         for reader, d in stack:
             reader(d["hidden"], d["ids"], d["weights"], out=d["out"])
-    timing = time_graph(graph, args.warmup, args.steps)
+    timing = time_graph(graph, args.warmup, args.steps, args.sample_seconds)
     ms_per_step = timing["ms_per_step"]
     us_per_layer = timing["ms_median"] * 1e3 / layers
     log(f"[{name}] {us_per_layer:.2f} us/layer (median of {PLAN_SAMPLES} samples of "
@@ -529,7 +532,8 @@ def summarize_trace(directory: str, command: str) -> str:
     """Per-kernel launch statistics of a rocprofv3 --kernel-trace --stats run."""
     durations: dict[str, list[int]] = {}
     reader_kernels = set(STAGE_KERNELS.values()) | {"select_all_kernel", "group_exact_kernel",
-                                                     "fused_screen_kernel", "output_wide_kernel"}
+                                                     "fused_screen_kernel", "output_wide_kernel",
+                                                     "output_staged_kernel"}
     for row in _rocprof_rows(directory, "kernel_trace.csv"):
         name = _short_name(row["Kernel_Name"])
         if name not in reader_kernels:
@@ -615,6 +619,8 @@ def main() -> int:
                         help="comma list of config:tokens[:retention[:screen_keep]] "
                              "measured beside the headline")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
+    parser.add_argument("--sample-seconds", type=float, default=PILOT_SECONDS,
+                        help="length of each timing sample (shorter under a profiler)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this reader runs without collectives; got --gpus {args.gpus}",
@@ -664,7 +670,7 @@ def main() -> int:
         "timing": {
             "value": f"median of {PLAN_SAMPLES} samples after the {args.warmup} warm-up replays, each "
                      f"sample {headline['replays_per_sample']} graph replays sized by a pilot of "
-                     f"about {PILOT_SECONDS} s (BASELINE.md section 3; the reference's "
+                     f"about {args.sample_seconds} s (BASELINE.md section 3; the reference's "
                      "scripts/speed_block.py:379-414), divided by the layers",
             "ms_per_step": f"mean of exactly {args.steps} replays between synchronisations",
             "stage_us": "each stage relaunched alone (cfmoe_launch_stage) 4 times over the stack's "
