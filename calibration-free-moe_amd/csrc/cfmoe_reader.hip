@@ -436,6 +436,11 @@ template <int kPrepareThreads, bool kIds64, bool kWeights16>
 __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const RouteShared &shared,
                                                 int *scratch) {
   constexpr int kPrepareWaves = kPrepareThreads / 64;
+  // (the arguments the routing uses, loaded in one batch at entry)
+  asm volatile("" ::"s"(a.router_ids), "s"(a.router_weights), "s"(a.padding_source), "s"(a.padding_bytes),
+               "s"(a.ids), "s"(a.weights), "s"(a.pair_tiles), "s"(a.group_pairs), "s"(a.group_experts),
+               "s"(a.group_starts), "s"(a.group_counts), "s"(a.group_total), "s"(a.T), "s"(a.K), "s"(a.E),
+               "s"(a.flags));
   int16_t *sorted = shared.sorted;
   int16_t *routed = shared.routed;
   int *counts = shared.counts, *base = shared.base;
@@ -446,73 +451,83 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
     return kWeights16 ? bf16f(load_global(static_cast<const uint16_t *>(a.router_weights) + q))
                       : load_global(static_cast<const float *>(a.router_weights) + q);
   };
-  // raw ids (outside [0, E) -> -1: no local expert, reads nothing); the
-  // formats are template arguments, so the loads of a batch of 8 pairs per
-  // thread are issued unconditionally (clamped index) and together
+  // Each thread's first kBatch pairs p = tid + kPrepareThreads q (all of
+  // them up to 8 pairs per thread: the host runs 1024 threads from 1024
+  // pairs unless the experts' LDS lists are too large): the raw ids, the
+  // router weights and the pairs' tokens' padding flags in one round trip,
+  // every load unconditional (clamped index; the formats are template
+  // arguments; a padding source of zero bytes reads zero: active)
   constexpr int kBatch = 8;
-  for (int q0 = 0; q0 * kPrepareThreads < pairs; q0 += kBatch) {
-    int raw_id[kBatch];
-#pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int p = min(tid + kPrepareThreads * (q0 + q), pairs - 1);
-      if (kIds64) {
-        const int32_t *words = static_cast<const int32_t *>(a.router_ids) + 2 * p;
-        const int low = load_global(words), high = load_global(words + 1);
-        raw_id[q] = high == (low >> 31) ? low : -1;  // outside the int32 range
-      } else {
-        raw_id[q] = load_global(static_cast<const int32_t *>(a.router_ids) + p);
-      }
+  const __amdgpu_buffer_rsrc_t padding = buffer_resource(a.padding_source, a.padding_bytes);
+  auto raw_id_of = [&](int p) {
+    if (kIds64) {
+      const int32_t *words = static_cast<const int32_t *>(a.router_ids) + 2 * p;
+      const int low = load_global(words), high = load_global(words + 1);
+      return high == (low >> 31) ? low : -1;  // outside the int32 range
     }
+    return load_global(static_cast<const int32_t *>(a.router_ids) + p);
+  };
+  auto store_routed = [&](int p, int raw) {
+    routed[p] = static_cast<int16_t>((raw < 0 || raw >= a.E) ? -1 : raw);
+    a.pair_tiles[p] = -1;  // pairs in no tile (padded token, no local expert)
+  };
+  int raw_id[kBatch];
+  float own_weight[kBatch];
+  uint32_t pad_flags[kBatch];
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int p = tid + kPrepareThreads * (q0 + q);
-      if (p < pairs) {
-        routed[p] = static_cast<int16_t>((raw_id[q] < 0 || raw_id[q] >= a.E) ? -1 : raw_id[q]);
-        a.pair_tiles[p] = -1;  // pairs in no tile (padded token, no local expert)
-      }
-    }
+  for (int q = 0; q < kBatch; ++q) {
+    const int p = min(tid + kPrepareThreads * q, pairs - 1);
+    raw_id[q] = raw_id_of(p);
+    own_weight[q] = weight_of(p);
+    pad_flags[q] = __builtin_amdgcn_raw_buffer_load_b8(padding, p / K, 0, 0);
   }
+  // (every load above is issued before the first is used)
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int q = 0; q < kBatch; ++q)
+    if (tid + kPrepareThreads * q < pairs) store_routed(tid + kPrepareThreads * q, raw_id[q]);
+  for (int p = tid + kBatch * kPrepareThreads; p < pairs; p += kPrepareThreads) store_routed(p, raw_id_of(p));
   __syncthreads();
   // slot k of a token moves to its rank among the token's ids (ties by slot);
   // its weight is the sum of the weights of equal ids (progressive.py:369-375)
-  for (int q0 = 0; q0 * kPrepareThreads < pairs; q0 += kBatch) {
-    float own_weight[kBatch];
+  int active_tokens = 0;  // tokens counted at their slot 0
+  auto place = [&](int p, float own, bool active) {
+    const int t = p / K, k = p % K;
+    active_tokens += k == 0 && active;
+    const int id = routed[p];
+    int rank = 0, equal = 0;
+    for (int j0 = 0; j0 < K; j0 += 8) {
+      int other[8];
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q)
-      own_weight[q] = weight_of(min(tid + kPrepareThreads * (q0 + q), pairs - 1));
+      for (int j = 0; j < 8; ++j) other[j] = routed[t * K + min(j0 + j, K - 1)];
 #pragma unroll
-    for (int q = 0; q < kBatch; ++q) {
-      const int p = tid + kPrepareThreads * (q0 + q);
-      if (p >= pairs) break;
-      const int t = p / K, k = p % K;
-      const bool active = is_active(a.padding, t);
-      const int id = routed[p];
-      int rank = 0, equal = 0;
-      for (int j0 = 0; j0 < K; j0 += 8) {
-        int other[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) other[j] = routed[t * K + min(j0 + j, K - 1)];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (j0 + j >= K) break;
-          rank += other[j] < id || (other[j] == id && j0 + j < k);
-          equal += other[j] == id;
-        }
+      for (int j = 0; j < 8; ++j) {
+        if (j0 + j >= K) break;
+        rank += other[j] < id || (other[j] == id && j0 + j < k);
+        equal += other[j] == id;
       }
-      float w = 0.0f;
-      if (active) {
-        if (equal == 1) {
-          w = 0.0f + own_weight[q];
-        } else {
-          for (int j = 0; j < K; ++j)
-            if (routed[t * K + j] == id) w += weight_of(t * K + j);
-        }
-      }
-      a.ids[t * K + rank] = id;
-      a.weights[t * K + rank] = w;
-      sorted[t * K + rank] = static_cast<int16_t>(active ? id : -1);
     }
+    float w = 0.0f;
+    if (active) {
+      if (equal == 1) {
+        w = 0.0f + own;
+      } else {
+        for (int j = 0; j < K; ++j)
+          if (routed[t * K + j] == id) w += weight_of(t * K + j);
+      }
+    }
+    a.ids[t * K + rank] = id;
+    a.weights[t * K + rank] = w;
+    sorted[t * K + rank] = static_cast<int16_t>(active ? id : -1);
+  };
+#pragma unroll
+  for (int q = 0; q < kBatch; ++q) {
+    const int p = tid + kPrepareThreads * q;
+    if (p >= pairs) break;
+    place(p, own_weight[q], pad_flags[q] == 0);
   }
+  for (int p = tid + kBatch * kPrepareThreads; p < pairs; p += kPrepareThreads)
+    place(p, weight_of(p), is_active(a.padding, p / K));
   const int padded = (pairs + 7) / 8 * 8;
   for (int p = pairs + tid; p < padded; p += kPrepareThreads) sorted[p] = -1;
   __syncthreads();
@@ -599,9 +614,7 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   // read statistics: one add per slot for all active tokens, then the
   // per-tile terms (integers, exact in FP64)
   if (a.flags & CFMOE_ACCOUNT) {
-    int active = 0;
-    for (int t = tid; t < T; t += kPrepareThreads) active += is_active(a.padding, t);
-    active = block_sum(active, scratch);
+    const int active = block_sum(active_tokens, scratch);
     if (tid < 18 && a.charges[tid] != 0.0 && active > 0)
       atomicAdd(a.read_work + tid, a.charges[tid] * static_cast<double>(active));
     const double tiles = static_cast<double>(total_tiles);

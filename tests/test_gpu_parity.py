@@ -364,6 +364,20 @@ def test_screen_splits_past_the_blocks_bit_exact(hidden, width, tokens, score):
     assert_parity(reader, out, expected, tokens)
 
 
+def test_routing_of_more_pairs_than_one_batch_per_thread():
+    """3072 experts and 4096 routed pairs: the experts' LDS lists keep the
+    routing block at 256 threads, so each thread routes 16 pairs, the first 8
+    from one round trip and the rest in further ones; padded tokens mixed in."""
+    tokens = 256
+    layer = make_layer(hidden=256, width=64, experts=3072, top_k=16, rank=8, tokens=tokens, seed=5)
+    plan = compile_budget(hidden_size=256, expert_width=64, top_k=16, retention=0.2, screen_keep=0.625)
+    padding = torch.zeros(tokens, dtype=torch.bool)
+    padding[::7] = True
+    reader = build(layer, plan, tokens, selection_score="point")
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights, padding)
+    assert_parity(reader, out, expected, tokens)
+
+
 def test_graph_replay_with_changing_inputs():
     tokens = 4
     layer = make_layer(hidden=512, width=256, experts=8, top_k=4, rank=16, tokens=tokens, seed=60)
