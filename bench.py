@@ -618,6 +618,10 @@ def main() -> int:
                                 "c5:1,c5:128,c5:1:0.123:1.0,c5:128:0.123:1.0",
                         help="comma list of config:tokens[:retention[:screen_keep]] "
                              "measured beside the headline")
+    parser.add_argument("--retention", type=float, default=0.0,
+                        help="the headline configuration's retention (0: the configuration's own)")
+    parser.add_argument("--keep", type=float, default=0.0,
+                        help="the headline configuration's screen keep (0: the configuration's own)")
     parser.add_argument("--cpu-seconds", type=float, default=10.0)
     parser.add_argument("--sample-seconds", type=float, default=PILOT_SECONDS,
                         help="length of each timing sample (shorter under a profiler)")
@@ -644,7 +648,8 @@ def main() -> int:
         extras.append(run_config(name, sub, device))
     probe = stream_probe(device)
     baseline = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
-    h, i, e, k, layers, tokens, retention, keep, description = CONFIGS[args.config]
+    h, i, e, k, layers, tokens, _, _, description = CONFIGS[args.config]
+    retention, keep = headline["retention"], headline["screen_keep"]
     kernel = stage_kernel(headline["dominant"], headline["tokens"])
     traffic = measured_traffic(kernel, args.config, headline["tokens"], headline["layers"])
     line = {
