@@ -627,81 +627,112 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   }
 }
 
-// The routing of a one-token call on one wave, in one round trip and without
-// barriers: the same lists as route_and_group. Lane k < K holds slot k's id
-// and weight; its rank among the token's ids (ties by slot) and the summed
-// weight of equal ids come from lane reads, each lane's sorted id travels to
-// its rank by a forward permute, and the runs of equal sorted ids (ascending,
-// absent slots first) are the experts' pair lists, cut into tiles of 16.
-__device__ __forceinline__ void route_single_token(const PrepareArgs &a) {
-  // (the arguments the stores and the accounting use, loaded in one batch)
-  asm volatile("" ::"s"(a.ids), "s"(a.weights), "s"(a.pair_tiles), "s"(a.group_pairs),
-               "s"(a.group_experts), "s"(a.group_starts), "s"(a.group_counts), "s"(a.group_total),
-               "s"(a.read_work), "s"(a.tile_sketch_bytes), "s"(a.tile_screen_macs),
-               "s"(a.tile_row_bytes), "s"(a.charges[0]), "s"(a.charges[1]), "s"(a.charges[2]),
-               "s"(a.charges[3]), "s"(a.charges[4]), "s"(a.charges[5]), "s"(a.charges[6]),
-               "s"(a.charges[7]), "s"(a.charges[8]), "s"(a.charges[9]), "s"(a.charges[10]),
-               "s"(a.charges[11]), "s"(a.charges[12]), "s"(a.charges[13]), "s"(a.charges[14]),
-               "s"(a.charges[15]), "s"(a.charges[16]), "s"(a.charges[17]));
+// One-token routing on one wave, in one round trip and without barriers (the
+// same lists as route_and_group). Lane k < K holds slot k's id and weight;
+// its rank among the token's ids (ties by slot) and the summed weight of
+// equal ids come from lane reads, each lane's sorted id travels to its rank
+// by a forward permute, and the runs of equal sorted ids (ascending, absent
+// slots first) are the experts' pair lists, cut into tiles of 16.
+//
+// The slot's id words, weight (both formats) and the token's padding flag:
+// buffer loads of every format, none behind a branch (a resource of zero
+// bytes reads zero: no padding mask means an active token).
+struct RouteLoads {
+  int word0, word1;
+  uint32_t weight_bits, weight_half, padded;
+};
+
+__device__ __forceinline__ RouteLoads route_loads(const PrepareArgs &a) {
   const int lane = threadIdx.x & 63;
   const int K = a.K;
-  const bool in = lane < K;
-  const int p = in ? lane : K - 1;
-  // the slot's id, weight and the token's padding flag in one round trip:
-  // buffer loads of every format, none behind a branch (a resource of zero
-  // bytes reads zero: no padding mask means an active token)
+  const int p = lane < K ? lane : K - 1;
   const bool ids64 = (a.flags & CFMOE_IDS_INT64) != 0, weights16 = (a.flags & CFMOE_WEIGHTS_BF16) != 0;
   const __amdgpu_buffer_rsrc_t ids = buffer_resource(a.router_ids, K * (ids64 ? 8 : 4));
   const __amdgpu_buffer_rsrc_t weights = buffer_resource(a.router_weights, K * (weights16 ? 2 : 4));
   const __amdgpu_buffer_rsrc_t padding = buffer_resource(a.padding_source, a.padding_bytes);
-  const int word0 = __builtin_amdgcn_raw_buffer_load_b32(ids, (ids64 ? 8 : 4) * p, 0, 0);
-  const int word1 = __builtin_amdgcn_raw_buffer_load_b32(ids, 8 * p + 4, 0, 0);
-  const uint32_t weight_bits = __builtin_amdgcn_raw_buffer_load_b32(weights, 4 * p, 0, 0);
-  const uint32_t weight_half = __builtin_amdgcn_raw_buffer_load_b16(weights, 2 * p, 0, 0);
-  const uint32_t padded = __builtin_amdgcn_raw_buffer_load_b8(padding, 0, 0, 0);
-  asm volatile("" ::"v"(word0), "v"(word1), "v"(weight_bits), "v"(weight_half), "v"(padded));
+  RouteLoads l;
+  l.word0 = __builtin_amdgcn_raw_buffer_load_b32(ids, (ids64 ? 8 : 4) * p, 0, 0);
+  l.word1 = __builtin_amdgcn_raw_buffer_load_b32(ids, 8 * p + 4, 0, 0);
+  l.weight_bits = __builtin_amdgcn_raw_buffer_load_b32(weights, 4 * p, 0, 0);
+  l.weight_half = __builtin_amdgcn_raw_buffer_load_b16(weights, 2 * p, 0, 0);
+  l.padded = __builtin_amdgcn_raw_buffer_load_b8(padding, 0, 0, 0);
+  return l;
+}
+
+// The token's routing as lane values: lane k < K holds slot k's id and its
+// sorted position (rank); lane q holds the sorted id at position q (-1:
+// absent, a padded token, or q >= K), the routed weight there, its run of
+// equal ids and its tile slot; `starts` marks the positions that start a tile.
+struct TokenRoute {
+  int id, rank, sorted, run_end, at;
+  float weight;
+  bool active, valid, tile_start;
+  uint64_t starts;
+};
+
+__device__ __forceinline__ TokenRoute route_token(const PrepareArgs &a, const RouteLoads &l) {
+  const int lane = threadIdx.x & 63;
+  const int K = a.K;
+  const bool in = lane < K;
+  const bool ids64 = (a.flags & CFMOE_IDS_INT64) != 0, weights16 = (a.flags & CFMOE_WEIGHTS_BF16) != 0;
   // (ids outside the int32 range are absent)
-  const int raw = !ids64 ? word0 : word1 == (word0 >> 31) ? word0 : -1;
-  const float weight = weights16 ? bf16f(static_cast<uint16_t>(weight_half)) : __uint_as_float(weight_bits);
-  const bool active = __builtin_amdgcn_readfirstlane(padded) == 0;
-  const int id = (raw < 0 || raw >= a.E) ? -1 : raw;
+  const int raw = !ids64 ? l.word0 : l.word1 == (l.word0 >> 31) ? l.word0 : -1;
+  const float weight = weights16 ? bf16f(static_cast<uint16_t>(l.weight_half)) : __uint_as_float(l.weight_bits);
+  TokenRoute r;
+  r.active = __builtin_amdgcn_readfirstlane(l.padded) == 0;
+  r.id = (raw < 0 || raw >= a.E) ? -1 : raw;
   int rank = 0;
   float w = 0.0f;  // sum of the weights of equal ids in slot order
   for (int j = 0; j < K; ++j) {
-    const int other = __builtin_amdgcn_readlane(id, j);
+    const int other = __builtin_amdgcn_readlane(r.id, j);
     const float other_weight = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), j));
-    rank += other < id || (other == id && j < lane);
-    if (other == id) w += other_weight;
+    rank += other < r.id || (other == r.id && j < lane);
+    if (other == r.id) w += other_weight;
   }
-  if (!active) w = 0.0f;
-  if (in) {
-    a.ids[rank] = id;
-    a.weights[rank] = w;
-  }
-  // lane q: the sorted id at position q (-1: absent, or a padded token)
-  int sorted = __builtin_amdgcn_ds_permute(4 * (in ? rank : lane), active ? id : -1);
+  if (!r.active) w = 0.0f;
+  r.rank = rank;
+  // lane q: the sorted id and routed weight at position q
+  const int target = 4 * (in ? rank : lane);
+  int sorted = __builtin_amdgcn_ds_permute(target, r.active ? r.id : -1);
+  r.weight = __int_as_float(__builtin_amdgcn_ds_permute(target, __float_as_int(w)));
   sorted = in ? sorted : -1;
-  const bool valid = sorted >= 0;
+  r.sorted = sorted;
+  r.valid = sorted >= 0;
   const int before = __shfl(sorted, max(lane - 1, 0));
-  const uint64_t heads = __ballot(valid && (lane == 0 || before != sorted));
+  const uint64_t heads = __ballot(r.valid && (lane == 0 || before != sorted));
   const uint64_t upto = lane == 63 ? ~0ull : (2ull << lane) - 1ull;  // lanes 0 .. lane
-  const int run_start = valid ? 63 - __builtin_clzll(heads & upto) : 0;
+  const int run_start = r.valid ? 63 - __builtin_clzll(heads & upto) : 0;
   const uint64_t later = heads & ~upto;
-  const int run_end = later ? __builtin_ctzll(later) : K;
+  r.run_end = later ? __builtin_ctzll(later) : K;
   const int offset = lane - run_start;
-  const bool tile_start = valid && offset % kGroupPairs == 0;
-  const uint64_t starts = __ballot(tile_start);
-  const int z = __popcll(starts & upto) - 1;
-  const int at = kGroupPairs * z + offset % kGroupPairs;
-  if (in) a.pair_tiles[lane] = valid ? at : -1;
-  if (valid) a.group_pairs[at] = lane;
-  if (tile_start) {
-    a.group_experts[z] = sorted;
-    a.group_starts[z] = kGroupPairs * z;
-    a.group_counts[z] = min(kGroupPairs, run_end - lane);
+  r.tile_start = r.valid && offset % kGroupPairs == 0;
+  r.starts = __ballot(r.tile_start);
+  const int z = __popcll(r.starts & upto) - 1;
+  r.at = kGroupPairs * z + offset % kGroupPairs;
+  return r;
+}
+
+// The routing outputs of a one-token call: sorted ids and weights, each
+// pair's tile slot, the tile lists (the runs of equal sorted ids, absent
+// slots first, cut into tiles of 16), the tile count and the accounting.
+__device__ __forceinline__ void store_token_route(const PrepareArgs &a, const TokenRoute &r) {
+  const int lane = threadIdx.x & 63;
+  const bool in = lane < a.K;
+  if (in) {
+    a.ids[r.rank] = r.id;
+    a.weights[lane] = r.weight;
+    a.pair_tiles[lane] = r.valid ? r.at : -1;
   }
-  const int total_tiles = __popcll(starts);
+  if (r.valid) a.group_pairs[r.at] = lane;
+  if (r.tile_start) {
+    const int z = r.at / kGroupPairs;
+    a.group_experts[z] = r.sorted;
+    a.group_starts[z] = kGroupPairs * z;
+    a.group_counts[z] = min(kGroupPairs, r.run_end - lane);
+  }
+  const int total_tiles = __popcll(r.starts);
   if (lane == 0) *a.group_total = total_tiles;
+  const bool active = r.active;
   if (a.flags & CFMOE_ACCOUNT) {
     // (uniform indices: the charges stay kernel arguments, not private memory)
 #pragma unroll
@@ -717,45 +748,44 @@ __device__ __forceinline__ void route_single_token(const PrepareArgs &a) {
   }
 }
 
-template <int kPrepareThreads>
-__global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
-  constexpr int kPrepareWaves = kPrepareThreads / 64;
-  // block 0 routes and groups (the longest block, dispatched first)
-  extern __shared__ __align__(16) char route_lds[];
-  __shared__ int route_scratch[32];
-  if (a.route && blockIdx.x == 0 && a.T == 1) {
-    if (threadIdx.x < 64) route_single_token(a);
-    return;
-  }
-  if (a.route && blockIdx.x == 0) {
-    const RouteShared shared = route_layout(route_lds, a.T * a.K, a.E);
-    if (a.flags & CFMOE_IDS_INT64) {
-      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<kPrepareThreads, true, true>(a, shared, route_scratch);
-      else route_and_group<kPrepareThreads, true, false>(a, shared, route_scratch);
-    } else {
-      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<kPrepareThreads, false, true>(a, shared, route_scratch);
-      else route_and_group<kPrepareThreads, false, false>(a, shared, route_scratch);
-    }
-    return;
-  }
-  const int cell_block = static_cast<int>(blockIdx.x) - (a.route ? 1 : 0);
-  __shared__ float compact_all[kPrepareWaves][128];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  // waves past the last cell still reach the block barrier below
-  const int cell_id = min(cell_block * kPrepareWaves + wave, a.cells - 1);
-  const bool owner = cell_block * kPrepareWaves + wave < a.cells;
-  const int B = a.H / 128;
-  const int t = cell_id / B, b = cell_id % B;
-  float *compact = compact_all[wave];
-  const bool active = is_active(a.padding, t);
-  if (!a.rotate) return;
+// The routing of a one-token call on one wave, in one round trip and without
+// barriers: the same lists as route_and_group.
+__device__ __forceinline__ void route_single_token(const PrepareArgs &a) {
+  // (the arguments the stores and the accounting use, loaded in one batch)
+  asm volatile("" ::"s"(a.ids), "s"(a.weights), "s"(a.pair_tiles), "s"(a.group_pairs),
+               "s"(a.group_experts), "s"(a.group_starts), "s"(a.group_counts), "s"(a.group_total),
+               "s"(a.read_work), "s"(a.tile_sketch_bytes), "s"(a.tile_screen_macs),
+               "s"(a.tile_row_bytes), "s"(a.charges[0]), "s"(a.charges[1]), "s"(a.charges[2]),
+               "s"(a.charges[3]), "s"(a.charges[4]), "s"(a.charges[5]), "s"(a.charges[6]),
+               "s"(a.charges[7]), "s"(a.charges[8]), "s"(a.charges[9]), "s"(a.charges[10]),
+               "s"(a.charges[11]), "s"(a.charges[12]), "s"(a.charges[13]), "s"(a.charges[14]),
+               "s"(a.charges[15]), "s"(a.charges[16]), "s"(a.charges[17]));
+  const RouteLoads l = route_loads(a);
+  asm volatile("" ::"v"(l.word0), "v"(l.word1), "v"(l.weight_bits), "v"(l.weight_half), "v"(l.padded));
+  store_token_route(a, route_token(a, l));
+}
 
-  const int H = a.H, keep = a.keep;
-  const int base = b * 128;
-  float v0 = active ? bf16f(a.x[static_cast<long>(t) * H + base + lane]) : 0.0f;
-  float v1 = active ? bf16f(a.x[static_cast<long>(t) * H + base + 64 + lane]) : 0.0f;
-  v0 = v0 * static_cast<float>(a.signs[base + lane]);
-  v1 = v1 * static_cast<float>(a.signs[base + 64 + lane]);
+// One (token, 128-block) cell of the rotation on one wave (progressive.py:
+// 389-453): lanes hold coordinates lane and 64 + lane of the signed hidden
+// block. Seven butterflies on lane exchanges in xor order (lane_xor: the
+// FP32 sums of the xor tree) and the 1/sqrt(128) scale; the keep largest
+// magnitudes by bisection on their bits (ties to the lowest coordinate);
+// their 21-bit grid values on the kept peak's exponent, the grid sum and
+// (kNorm) the kept values' squared norm, summed in compacted order through
+// the wave's 128 floats of LDS. `sync` orders the wave's LDS writes before
+// its reads (a block barrier where every wave of the block calls it).
+struct Cell {
+  float v0, v1;
+  bool kept0, kept1;
+  int pos0, pos1;
+  int32_t q0, q1;
+  int shift, qsum;
+  float sq;
+};
+
+template <bool kNorm, class Sync>
+__device__ __forceinline__ Cell cell_grid(float v0, float v1, int keep, float *compact, Sync sync) {
+  const int lane = threadIdx.x & 63;
   // butterfly stage m: (l + r, l - r) of lanes l and l ^ m
   auto stage = [&](auto mask) {
     constexpr int kMask = decltype(mask)::value;
@@ -800,54 +830,109 @@ __global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a)
     kept0 = m0 > cutoff || (m0 == cutoff && rank0 < room);
     kept1 = m1 > cutoff || (m1 == cutoff && rank1 < room);
   }
+  Cell c;
+  c.v0 = v0;
+  c.v1 = v1;
+  c.kept0 = kept0;
+  c.kept1 = kept1;
   const uint64_t k0 = __ballot(kept0), k1 = __ballot(kept1);
-  const int pos0 = __popcll(k0 & lanes_below(lane));
-  const int pos1 = __popcll(k0) + __popcll(k1 & lanes_below(lane));
-  if (kept0) compact[pos0] = v0;
-  if (kept1) compact[pos1] = v1;
-  __syncthreads();
-  if (!owner) return;
-  const long cell = static_cast<long>(t) * B + b;
-  float sq = lane < keep ? compact[lane] * compact[lane] : 0.0f;
-  if (lane + 64 < keep) sq = fmaf(compact[lane + 64], compact[lane + 64], sq);
-  // (the xor-butterfly sum over the lanes, levels m = 1, 2, ..., 32)
-  sq = wave_sum_lane0(sq);
+  c.pos0 = __popcll(k0 & lanes_below(lane));
+  c.pos1 = __popcll(k0) + __popcll(k1 & lanes_below(lane));
+  c.sq = 0.0f;
+  if (kNorm) {
+    if (kept0) compact[c.pos0] = v0;
+    if (kept1) compact[c.pos1] = v1;
+    sync();
+    float sq = lane < keep ? compact[lane] * compact[lane] : 0.0f;
+    if (lane + 64 < keep) sq = fmaf(compact[lane + 64], compact[lane + 64], sq);
+    // (the xor-butterfly sum over the lanes, levels m = 1, 2, ..., 32)
+    c.sq = wave_sum_lane0(sq);
+  }
   const uint32_t peak = wave_extreme<true>(max(kept0 ? m0 : 0u, kept1 ? m1 : 0u));
   int exponent = 0;
   if (peak) frexpf(__uint_as_float(peak), &exponent);
-  const int shift = peak ? 20 - exponent : 0;
-  const int32_t q0 = kept0 && peak ? static_cast<int32_t>(rintf(ldexpf(v0, shift))) : 0;
-  const int32_t q1 = kept1 && peak ? static_cast<int32_t>(rintf(ldexpf(v1, shift))) : 0;
+  c.shift = peak ? 20 - exponent : 0;
+  c.q0 = kept0 && peak ? static_cast<int32_t>(rintf(ldexpf(v0, c.shift))) : 0;
+  c.q1 = kept1 && peak ? static_cast<int32_t>(rintf(ldexpf(v1, c.shift))) : 0;
   // sum of the cell's grid values (exact in any order: |q| <= 2^20, 128 values)
-  const int qsum = wave_sum_all(q0 + q1);
+  c.qsum = wave_sum_all(c.q0 + c.q1);
+  return c;
+}
+
+// A cell's rotated plane, kept coordinates, grid values and digit planes,
+// its grid sum, exponent and kept norm (lane 0) into the workspace.
+__device__ __forceinline__ void store_cell(const PrepareArgs &a, long cell, const Cell &c) {
+  const int lane = threadIdx.x & 63, keep = a.keep;
   if (lane == 0) {
-    a.norm2[cell] = sq;
-    a.qexp[cell] = shift;
-    a.qsums[cell] = qsum;
+    a.norm2[cell] = c.sq;
+    a.qexp[cell] = c.shift;
+    a.qsums[cell] = c.qsum;
   }
-  if (kept0) {
-    a.planes[cell * keep + pos0] = v0;
-    a.qvals[cell * keep + pos0] = q0;
-    if (keep < 128) a.coords[cell * keep + pos0] = lane;
+  if (c.kept0) {
+    a.planes[cell * keep + c.pos0] = c.v0;
+    a.qvals[cell * keep + c.pos0] = c.q0;
+    if (keep < 128) a.coords[cell * keep + c.pos0] = lane;
   }
-  if (kept1) {
-    a.planes[cell * keep + pos1] = v1;
-    a.qvals[cell * keep + pos1] = q1;
-    if (keep < 128) a.coords[cell * keep + pos1] = 64 + lane;
+  if (c.kept1) {
+    a.planes[cell * keep + c.pos1] = c.v1;
+    a.qvals[cell * keep + c.pos1] = c.q1;
+    if (keep < 128) a.coords[cell * keep + c.pos1] = 64 + lane;
   }
   // the dense digit planes the screen stages (zero where not kept: q = 0)
-  {
-    int8_t *row = a.digits + cell * 3 * 128;
-    int d0, d1, d2;
-    grid_digits(q0, d0, d1, d2);
-    row[lane] = static_cast<int8_t>(d0);
-    row[128 + lane] = static_cast<int8_t>(d1);
-    row[256 + lane] = static_cast<int8_t>(d2);
-    grid_digits(q1, d0, d1, d2);
-    row[64 + lane] = static_cast<int8_t>(d0);
-    row[192 + lane] = static_cast<int8_t>(d1);
-    row[320 + lane] = static_cast<int8_t>(d2);
+  int8_t *row = a.digits + cell * 3 * 128;
+  int d0, d1, d2;
+  grid_digits(c.q0, d0, d1, d2);
+  row[lane] = static_cast<int8_t>(d0);
+  row[128 + lane] = static_cast<int8_t>(d1);
+  row[256 + lane] = static_cast<int8_t>(d2);
+  grid_digits(c.q1, d0, d1, d2);
+  row[64 + lane] = static_cast<int8_t>(d0);
+  row[192 + lane] = static_cast<int8_t>(d1);
+  row[320 + lane] = static_cast<int8_t>(d2);
+}
+
+template <int kPrepareThreads>
+__global__ __launch_bounds__(kPrepareThreads) void prepare_kernel(PrepareArgs a) {
+  constexpr int kPrepareWaves = kPrepareThreads / 64;
+  // block 0 routes and groups (the longest block, dispatched first)
+  extern __shared__ __align__(16) char route_lds[];
+  __shared__ int route_scratch[32];
+  if (a.route && blockIdx.x == 0 && a.T == 1) {
+    if (threadIdx.x < 64) route_single_token(a);
+    return;
   }
+  if (a.route && blockIdx.x == 0) {
+    const RouteShared shared = route_layout(route_lds, a.T * a.K, a.E);
+    if (a.flags & CFMOE_IDS_INT64) {
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<kPrepareThreads, true, true>(a, shared, route_scratch);
+      else route_and_group<kPrepareThreads, true, false>(a, shared, route_scratch);
+    } else {
+      if (a.flags & CFMOE_WEIGHTS_BF16) route_and_group<kPrepareThreads, false, true>(a, shared, route_scratch);
+      else route_and_group<kPrepareThreads, false, false>(a, shared, route_scratch);
+    }
+    return;
+  }
+  const int cell_block = static_cast<int>(blockIdx.x) - (a.route ? 1 : 0);
+  __shared__ float compact_all[kPrepareWaves][128];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // waves past the last cell still reach the block barrier below
+  const int cell_id = min(cell_block * kPrepareWaves + wave, a.cells - 1);
+  const bool owner = cell_block * kPrepareWaves + wave < a.cells;
+  const int B = a.H / 128;
+  const int t = cell_id / B, b = cell_id % B;
+  float *compact = compact_all[wave];
+  const bool active = is_active(a.padding, t);
+  if (!a.rotate) return;
+
+  const int H = a.H, keep = a.keep;
+  const int base = b * 128;
+  const float v0 = active ? bf16f(a.x[static_cast<long>(t) * H + base + lane]) : 0.0f;
+  const float v1 = active ? bf16f(a.x[static_cast<long>(t) * H + base + 64 + lane]) : 0.0f;
+  const Cell cell = cell_grid<true>(v0 * static_cast<float>(a.signs[base + lane]),
+                                    v1 * static_cast<float>(a.signs[base + 64 + lane]), keep, compact,
+                                    [] { __syncthreads(); });
+  if (!owner) return;
+  store_cell(a, static_cast<long>(t) * B + b, cell);
 }
 
 // ---------------------------------------------------------------------------
@@ -1350,7 +1435,6 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
                     beta);
   }
 }
-
 
 // ---------------------------------------------------------------------------
 // Fused screen and score for grouped batches (progressive.py:2428-2606 and
@@ -3246,10 +3330,10 @@ long down_order_words(long capacity, const Shape &s) {
 }
 
 
-int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
-                   const cfmoe_workspace *ws, const void *hidden, const void *router_ids,
-                   const void *router_weights, const uint8_t *padding, int tokens,
-                   const double *charges, bool route, bool rotate, hipStream_t stream) {
+PrepareArgs prepare_args(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
+                         const cfmoe_workspace *ws, const void *hidden, const void *router_ids,
+                         const void *router_weights, const uint8_t *padding, int tokens,
+                         const double *charges, bool route, bool rotate) {
   PrepareArgs a;
   memset(&a, 0, sizeof(a));
   a.x = static_cast<const uint16_t *>(hidden);
@@ -3299,6 +3383,15 @@ int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
   a.route = route;
   a.rotate = rotate;
   a.cells = tokens * (rotate ? s.B : 1);
+  return a;
+}
+
+int launch_prepare(const Shape &s, const cfmoe_dims *d, const cfmoe_weights *w,
+                   const cfmoe_workspace *ws, const void *hidden, const void *router_ids,
+                   const void *router_weights, const uint8_t *padding, int tokens,
+                   const double *charges, bool route, bool rotate, hipStream_t stream) {
+  const PrepareArgs a =
+      prepare_args(s, d, w, ws, hidden, router_ids, router_weights, padding, tokens, charges, route, rotate);
   const int pairs = tokens * s.K;
   const bool wide = route && pairs >= kWidePreparePairs &&
                     route_lds_bytes(pairs, d->experts, kWidePrepareThreads / 64) <= 96 * 1024;
@@ -3433,6 +3526,44 @@ int cfmoe_prepare_input(const cfmoe_dims *dims, const cfmoe_weights *weights,
 
 namespace cfmoe {
 
+static SmallScreenArgs small_screen_args(const Shape &s, const cfmoe_dims *dims, const cfmoe_weights *weights,
+                                         const cfmoe_workspace *workspace, const uint8_t *padding,
+                                         int32_t tokens) {
+  const uint32_t flags = dims->flags;
+  SmallScreenArgs ss;
+  ss.planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
+  ss.stats = static_cast<const uint16_t *>(weights->statistics);
+  ss.digits = workspace->digits;
+  ss.qexp = workspace->qexp;
+  ss.qsums = workspace->qsums;
+  ss.norm2 = workspace->norm2;
+  ss.group_experts = workspace->group_experts;
+  ss.group_counts = workspace->group_counts;
+  ss.group_pairs = workspace->group_pairs;
+  ss.group_total = workspace->group_total;
+  ss.ids = workspace->ids;
+  ss.weights = workspace->weights;
+  ss.padding = padding;
+  ss.norms = weights->norms;
+  ss.geometry = (flags & CFMOE_GEOMETRY) ? weights->geometry : nullptr;
+  ss.partial = workspace->partial;
+  ss.variances = workspace->variances;
+  ss.scores = workspace->scores;
+  ss.H = s.H;
+  ss.I = s.I;
+  ss.K = s.K;
+  ss.N = s.N;
+  ss.T = tokens;
+  ss.splits = s.splits;
+  ss.span = s.span;
+  ss.tile_items = static_cast<int>(tile_bound(tokens, s.K, dims->experts)) * (s.I / kRowTile);
+  // a tile holds at most 16 pairs, and at most tokens * K
+  ss.max_pairs = static_cast<int>(std::min<long>(kPairTile, static_cast<long>(tokens) * s.K));
+  ss.gelu = (flags & CFMOE_GELU) != 0;
+  ss.point = (flags & CFMOE_POINT) != 0;
+  return ss;
+}
+
 static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weights *weights,
                       const cfmoe_workspace *workspace, const void *hidden,
                       const void *router_ids, const void *router_weights,
@@ -3553,37 +3684,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
         hipLaunchKernelGGL((fused_screen_kernel<false, kMaxSpan>), dim3(blocks), dim3(kFusedThreads), 0, stream, fs);
       if ((rc = check_launch("screen"))) return rc;
     } else if (stages & (1u << CFMOE_STAGE_SCREEN)) {
-      SmallScreenArgs ss;
-      ss.planes = trit_planes;
-      ss.stats = statistics;
-      ss.digits = workspace->digits;
-      ss.qexp = workspace->qexp;
-      ss.qsums = workspace->qsums;
-      ss.norm2 = workspace->norm2;
-      ss.group_experts = workspace->group_experts;
-      ss.group_counts = workspace->group_counts;
-      ss.group_pairs = workspace->group_pairs;
-      ss.group_total = workspace->group_total;
-      ss.ids = workspace->ids;
-      ss.weights = workspace->weights;
-      ss.padding = padding;
-      ss.norms = weights->norms;
-      ss.geometry = (flags & CFMOE_GEOMETRY) ? weights->geometry : nullptr;
-      ss.partial = workspace->partial;
-      ss.variances = workspace->variances;
-      ss.scores = workspace->scores;
-      ss.H = s.H;
-      ss.I = s.I;
-      ss.K = s.K;
-      ss.N = s.N;
-      ss.T = tokens;
-      ss.splits = s.splits;
-      ss.span = s.span;
-      ss.tile_items = static_cast<int>(tiles) * (s.I / kRowTile);
-      // a tile holds at most 16 pairs, and at most tokens * K
-      ss.max_pairs = static_cast<int>(std::min<long>(kPairTile, static_cast<long>(tokens) * s.K));
-      ss.gelu = gelu;
-      ss.point = !gh5;
+      const SmallScreenArgs ss = small_screen_args(s, dims, weights, workspace, padding, tokens);
       const unsigned blocks = static_cast<unsigned>(ss.tile_items + tokens);
       const bool narrow = s.span <= kNarrowSpan;
       const unsigned lds = static_cast<unsigned>(small_screen_lds(ss.max_pairs, narrow ? kNarrowSpan : kMaxSpan));
