@@ -292,6 +292,13 @@ class ReaderWorkspace:
         )
         self.bytes = sum(t.numel() * t.element_size() for t in buffers)
         self.charged = False
+        # prepare_input's side stream (default priority) and its two events
+        # (progressive.py:3113-3121), made on first use; `input_pending` is
+        # set while a preparation awaits its consuming call
+        self.input_stream: torch.cuda.Stream | None = None
+        self.input_ready: torch.cuda.Event | None = None
+        self.input_done: torch.cuda.Event | None = None
+        self.input_pending = False
 
     def pointers(self, read_work: Tensor, final_count: int | None = None) -> _ext.WorkspacePointers:
         """C view of the buffers; `final_count` re-views the kept-id list."""
@@ -781,15 +788,26 @@ class ProgressiveReader:
     def prepare_input(self, hidden: Tensor, padding: Tensor | None = None) -> bool:
         """Rotate the input ahead of the router (progressive.py:3829-3873).
 
-        Enqueued on the current stream. Returns False, launching nothing, for
+        The rotation runs on the workspace's side stream once the current
+        stream has reached this point, so it overlaps whatever the caller
+        enqueues next (the router). Returns False, launching nothing, for
         unscreened plans. Pass input_prepared=True to the next call with the
-        same rows; the workspace stays non-reentrant in between.
+        same rows: that call makes the current stream wait for the rotation
+        before its first kernel. The workspace stays non-reentrant in
+        between.
         """
         p = self.plan
         if p.completion_count == p.candidate_count:
             return False
         tokens = self._validate_input(hidden, padding)
         dims = _dims(p, self.native_gu.shape[0], self.rank, 0, self.grouped_tokens)
+        w = self.workspace
+        device = self.native_gu.device
+        if w.input_stream is None:
+            w.input_stream = torch.cuda.Stream(device=device)
+            w.input_ready, w.input_done = torch.cuda.Event(), torch.cuda.Event()
+        w.input_ready.record(torch.cuda.current_stream(device))
+        w.input_stream.wait_event(w.input_ready)
         _ext.check(
             _ext.library().cfmoe_prepare_input(
                 ctypes.byref(dims),
@@ -798,10 +816,19 @@ class ProgressiveReader:
                 hidden.data_ptr(),
                 _pointer(padding),
                 tokens,
-                self._stream(),
+                w.input_stream.cuda_stream,
             )
         )
+        w.input_done.record(w.input_stream)
+        w.input_pending = True
         return True
+
+    def _join_input(self) -> None:
+        """The current stream waits for a pending prepare_input rotation."""
+        w = self.workspace
+        if w.input_pending:
+            torch.cuda.current_stream(self.native_gu.device).wait_event(w.input_done)
+            w.input_pending = False
 
     @torch.no_grad()
     def __call__(
@@ -847,6 +874,8 @@ class ProgressiveReader:
         if out is None:
             out = torch.empty_like(hidden)
         dims = self._call_dims(ids, weights, input_prepared)
+        if input_prepared:
+            self._join_input()
         _ext.check(
             _ext.library().cfmoe_forward(
                 ctypes.byref(dims),

@@ -56,6 +56,58 @@ def test_prepared_input_equals_a_plain_call(tokens):
     assert_parity(reader, out, expected, tokens)
 
 
+@pytest.mark.parametrize("tokens", [1, 20])
+def test_prepared_input_runs_on_the_side_stream(tokens):
+    """prepare_input rotates on the workspace's side stream while the current
+    stream runs what the caller enqueues next (the router's place); the
+    prepared call waits for it. Eagerly and captured in a HIP graph (the side
+    stream forks from and joins the capture), replayed with new rows and
+    padding, every result equals a plain call bit for bit."""
+    layer = make_layer(hidden=512, width=256, experts=16, top_k=4, rank=16, tokens=tokens,
+                       seed=110 + tokens)
+    plan = compile_budget(hidden_size=512, expert_width=256, top_k=4, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    x = layer.hidden.to(DEVICE).clone()
+    ids, weights = layer.ids.to(DEVICE), layer.weights.to(DEVICE)
+    padding = torch.zeros(tokens, dtype=torch.bool, device=DEVICE)
+    padding[-1] = tokens > 1
+    router = torch.randn(512, 16, generator=torch.Generator().manual_seed(5)).to(DEVICE)
+    assert reader.prepare_input(x, padding)
+    side = reader.workspace.input_stream
+    assert side is not None and side != torch.cuda.current_stream()
+    logits = torch.mm(x.float(), router)
+    prepared = reader(x, ids, weights, padding, input_prepared=True)
+    torch.cuda.synchronize()
+    assert not reader.workspace.input_pending
+    plain = reader(x, ids, weights, padding)
+    torch.cuda.synchronize()
+    assert torch.equal(prepared, plain)
+    assert torch.isfinite(logits).all()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert reader.prepare_input(x, padding)
+        scaled = x.float().mul(0.5)
+        captured = reader(x, ids, weights, padding, input_prepared=True)
+    generator = torch.Generator().manual_seed(11)
+    for replay in range(3):
+        x.copy_(torch.randn(tokens, 512, generator=generator).bfloat16())
+        padding.zero_()
+        padding[0] = replay == 1
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(scaled, x.float().mul(0.5))
+        plain = reader(x, ids, weights, padding)
+        torch.cuda.synchronize()
+        assert torch.equal(captured, plain), f"replay {replay}"
+    # the last plain call left this batch's state: the oracle holds it too
+    _, expected = run_both(reader, layer, plan, x.cpu(), layer.ids, layer.weights, padding.cpu())
+    assert reader.prepare_input(x, padding)
+    out = reader(x, ids, weights, padding, input_prepared=True)
+    torch.cuda.synchronize()
+    assert_parity(reader, out, expected, tokens)
+
+
 def test_prepare_input_is_a_no_op_for_a_dense_plan():
     layer = make_layer(hidden=256, width=64, experts=4, top_k=2, rank=8, tokens=2, seed=104)
     plan = compile_budget(hidden_size=256, expert_width=64, top_k=2, retention=1.0)
