@@ -483,17 +483,38 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   }
   // (every load above is issued before the first is used)
   asm volatile("" ::: "memory");
+  int active_tokens = 0;  // tokens counted at their slot 0
 #pragma unroll
-  for (int q = 0; q < kBatch; ++q)
-    if (tid + kPrepareThreads * q < pairs) store_routed(tid + kPrepareThreads * q, raw_id[q]);
-  for (int p = tid + kBatch * kPrepareThreads; p < pairs; p += kPrepareThreads) store_routed(p, raw_id_of(p));
+  for (int q = 0; q < kBatch; ++q) {
+    const int p = tid + kPrepareThreads * q;
+    if (p < pairs) {
+      store_routed(p, raw_id[q]);
+      active_tokens += p % K == 0 && pad_flags[q] == 0;
+    }
+  }
+  for (int p = tid + kBatch * kPrepareThreads; p < pairs; p += kPrepareThreads) {
+    store_routed(p, raw_id_of(p));
+    active_tokens += p % K == 0 && is_active(a.padding, p / K);
+  }
+  // the fixed read charges go out right after the first barrier, so their
+  // atomics travel while the routing runs (the wave sums cross it in scratch)
+  const bool account = (a.flags & CFMOE_ACCOUNT) != 0;
+  if (account) {
+    const int wave_active = wave_sum_all(active_tokens);
+    if ((tid & 63) == 0) scratch[tid >> 6] = wave_active;
+  }
   __syncthreads();
+  if (account && tid < 18) {
+    int active = 0;
+#pragma unroll
+    for (int w = 0; w < kPrepareWaves; ++w) active += scratch[w];
+    if (a.charges[tid] != 0.0 && active > 0)
+      atomicAdd(a.read_work + tid, a.charges[tid] * static_cast<double>(active));
+  }
   // slot k of a token moves to its rank among the token's ids (ties by slot);
   // its weight is the sum of the weights of equal ids (progressive.py:369-375)
-  int active_tokens = 0;  // tokens counted at their slot 0
   auto place = [&](int p, float own, bool active) {
     const int t = p / K, k = p % K;
-    active_tokens += k == 0 && active;
     const int id = routed[p];
     int rank = 0, equal = 0;
     for (int j0 = 0; j0 < K; j0 += 8) {
@@ -558,6 +579,14 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
   int packed_total;  // members and tiles are below 2^16 (pairs <= 8192)
   const int packed = block_exclusive(members | (tiles << 16), scratch, &packed_total);
   const int total_tiles = packed_total >> 16;
+  // the per-tile read charges (integers, exact in FP64), issued as soon as
+  // the tile count is known
+  if (account && total_tiles > 0) {
+    const double tile_count = static_cast<double>(total_tiles);
+    if (tid == 32 && a.tile_sketch_bytes != 0.0) atomicAdd(a.read_work + 11, tile_count * a.tile_sketch_bytes);
+    if (tid == 33 && a.tile_screen_macs != 0.0) atomicAdd(a.read_work + 15, tile_count * a.tile_screen_macs);
+    if (tid == 34 && a.tile_row_bytes != 0.0) atomicAdd(a.read_work + 12, tile_count * a.tile_row_bytes);
+  }
   {
     int start = packed & 0xffff, z = packed >> 16;
     for (int e = first; e < last; ++e) {
@@ -611,20 +640,6 @@ __device__ __forceinline__ void route_and_group(const PrepareArgs &a, const Rout
     }
   }
   if (tid == 0) *a.group_total = total_tiles;
-  // read statistics: one add per slot for all active tokens, then the
-  // per-tile terms (integers, exact in FP64)
-  if (a.flags & CFMOE_ACCOUNT) {
-    const int active = block_sum(active_tokens, scratch);
-    if (tid < 18 && a.charges[tid] != 0.0 && active > 0)
-      atomicAdd(a.read_work + tid, a.charges[tid] * static_cast<double>(active));
-    const double tiles = static_cast<double>(total_tiles);
-    if (tid == 32 && a.tile_sketch_bytes != 0.0 && total_tiles > 0)
-      atomicAdd(a.read_work + 11, tiles * a.tile_sketch_bytes);
-    if (tid == 33 && a.tile_screen_macs != 0.0 && total_tiles > 0)
-      atomicAdd(a.read_work + 15, tiles * a.tile_screen_macs);
-    if (tid == 34 && a.tile_row_bytes != 0.0 && total_tiles > 0)
-      atomicAdd(a.read_work + 12, tiles * a.tile_row_bytes);
-  }
 }
 
 // One-token routing on one wave, in one round trip and without barriers (the
