@@ -792,9 +792,9 @@ class ProgressiveReader:
         stream has reached this point, so it overlaps whatever the caller
         enqueues next (the router). Returns False, launching nothing, for
         unscreened plans. Pass input_prepared=True to the next call with the
-        same rows: that call makes the current stream wait for the rotation
-        before its first kernel. The workspace stays non-reentrant in
-        between.
+        same rows. The next call on the workspace, prepared or not, makes the
+        current stream wait for the rotation before its first kernel; the
+        workspace stays non-reentrant in between.
         """
         p = self.plan
         if p.completion_count == p.candidate_count:
@@ -824,7 +824,8 @@ class ProgressiveReader:
         return True
 
     def _join_input(self) -> None:
-        """The current stream waits for a pending prepare_input rotation."""
+        """The current stream waits for a pending prepare_input rotation (any
+        call does: the rotation writes rows of the shared workspace)."""
         w = self.workspace
         if w.input_pending:
             torch.cuda.current_stream(self.native_gu.device).wait_event(w.input_done)
@@ -874,8 +875,9 @@ class ProgressiveReader:
         if out is None:
             out = torch.empty_like(hidden)
         dims = self._call_dims(ids, weights, input_prepared)
-        if input_prepared:
-            self._join_input()
+        # any call joins a pending rotation first: it reads or rewrites the
+        # same workspace rows
+        self._join_input()
         _ext.check(
             _ext.library().cfmoe_forward(
                 ctypes.byref(dims),
@@ -913,6 +915,7 @@ class ProgressiveReader:
         tokens = hidden.shape[0]
         flags = self._flags(ids, weights, False) & ~_ext.ACCOUNT
         dims = _dims(self.plan, self.native_gu.shape[0], self.rank, flags, self.grouped_tokens)
+        self._join_input()
         _ext.check(
             _ext.library().cfmoe_launch_stage(
                 _ext.STAGES.index(stage),

@@ -84,6 +84,14 @@ def test_prepared_input_runs_on_the_side_stream(tokens):
     torch.cuda.synchronize()
     assert torch.equal(prepared, plain)
     assert torch.isfinite(logits).all()
+    # a call that is not the prepared one still waits for a pending rotation
+    # (of other rows here) before it rewrites the same workspace rows
+    other = torch.randn(tokens, 512, generator=torch.Generator().manual_seed(9)).bfloat16().to(DEVICE)
+    assert reader.prepare_input(other, padding)
+    again = reader(x, ids, weights, padding)
+    torch.cuda.synchronize()
+    assert not reader.workspace.input_pending
+    assert torch.equal(again, plain)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         assert reader.prepare_input(x, padding)
