@@ -5,8 +5,9 @@ Drop-in for `calibration_free_moe/reader/progressive.py` of the reference
 call signature, attributes and `report()`, same `ReaderWorkspace`, same module
 names. The device work is done by hand-written HIP kernels for gfx950 in
 libcfmoe_reader.so (C ABI: include/cfmoe_reader.h), called through ctypes on
-the caller's current stream. There is no Triton, no CPU fallback: without the
-library every call raises RuntimeError.
+the caller's current stream (`prepare_input` on a side stream that the next
+call joins). There is no Triton, no CPU fallback: without the library every
+call raises RuntimeError.
 
 Stages of one call (reference progressive.py:13-24):
 
