@@ -342,11 +342,12 @@ __device__ int block_exclusive(int v, int *scratch, int *total) {
 // prepare: route + expert grouping (progressive.py:349-386, :2329-2373) and
 // rotate/mask (:389-453)
 //
-// 256-thread blocks. Block 0 sorts every token's K ids, groups the (token,
-// slot) pairs by expert into tiles of at most 16 pairs (touched experts in
-// ascending id order, each with its pairs in ascending pair index:
-// deterministic lists, no atomics in the order) and adds the fixed read
-// charges. Wave w of cell block i rotates cell 4 i + w = (token, block).
+// 256-thread blocks (1024 from kWidePreparePairs routed pairs). Block 0
+// sorts every token's K ids, groups the (token, slot) pairs by expert into
+// tiles of at most 16 pairs (touched experts in ascending id order, each with
+// its pairs in ascending pair index: deterministic lists, no atomics in the
+// order) and adds the fixed read charges. Wave w of cell block i rotates cell
+// W i + w = (token, block), W the block's waves.
 
 // Balanced 8-bit digits of a grid value: q = d0 + 2^8 d1 + 2^16 d2 with
 // d_i in [-128, 127] (|q| <= 2^20).
@@ -1175,7 +1176,7 @@ __device__ __forceinline__ ScoreInputs load_score_inputs(const Args &a, int e, i
 }
 
 template <bool kGh5, class Args>
-__device__ __forceinline__ void score_four(const Args &a, int e, int token, int slot, int c,
+__device__ __forceinline__ void score_four(const Args &a, int token, int slot, int c,
                                            const float gate[4], const float up[4],
                                            const float gate_var[4], const float up_var[4],
                                            const ScoreInputs &in) {
@@ -1216,8 +1217,8 @@ __device__ __forceinline__ void score_one(const Args &a, int token, int slot, in
 // ---------------------------------------------------------------------------
 // Screen and score below the grouped size (progressive.py:478-1108,
 // :1111-1353). Workgroup = (16-pair tile z, channel tile ct: gate row tile
-// ct and up row tile I/16 + ct); wave w takes the block splits
-// [w S / 4, (w + 1) S / 4) and stages, for the tile's live pairs only, those
+// ct and up row tile I/16 + ct); wave w of the eight takes the block splits
+// [w P, (w + 1) P), P = ceil(S / 8) (one split each at S <= 8), and stages, for the tile's live pairs only, those
 // blocks' digit planes in its own LDS area (no barrier: a wave reads only what
 // it wrote, and its LDS operations complete in order). Per split the wave
 // forms the partial (fma chain over the split's blocks) of its 2 x 4 rows for
@@ -1306,7 +1307,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
   int my_pair = slots[0];
 #pragma unroll
   for (int p = 1; p < kPairTile; ++p) my_pair = my_row == p ? slots[p] : my_pair;
-  const int my_token = my_pair / a.K, my_slot = my_pair % a.K;
+  const int my_token = my_pair / a.K;
   const int span = a.span, splits = a.splits;
   const int per_wave = (splits + kSmallWaves - 1) / kSmallWaves;
   const int s_begin = wave * per_wave, s_end = min(splits, s_begin + per_wave);
@@ -1745,14 +1746,15 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   // (the score's inputs here: held across the splits they would cost a wave per SIMD)
   const int c = kRowTile * ct + row_in_tile;
   const ScoreInputs inputs = load_score_inputs(a, e, sh.pair_token[pp], sh.pair_slot[pp], c);
-  score_four<kGh5>(a, e, sh.pair_token[pp], sh.pair_slot[pp], c, est[0], est[1], var[0], var[1],
+  score_four<kGh5>(a, sh.pair_token[pp], sh.pair_slot[pp], c, est[0], est[1], var[0], var[1],
                    inputs);
 }
 
 // ---------------------------------------------------------------------------
 // select (progressive.py:1584-1775): the F best keys of score + 0 per token,
-// ties to the lowest candidate id. Three radix passes (11/11/10 bits) find the
-// F-th largest key; a block scan compacts the kept ids in candidate order.
+// ties to the lowest candidate id. Two 12-bit radix passes (and an 8-bit one
+// when the cutoff's 24-bit bin holds more keys than remain) find the F-th
+// largest key; a block scan compacts the kept ids in candidate order.
 
 struct SelectArgs {
   const float *scores;
