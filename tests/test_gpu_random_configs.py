@@ -14,8 +14,8 @@ import pytest
 import torch
 
 from calibration_free_moe.reader.budget import compile_budget
-from tests.synthetic import make_layer
-from tests.test_gpu_parity import assert_parity, build, run_both
+from tests.synthetic import make_layer, make_routed_layer
+from tests.test_gpu_parity import DEVICE, assert_parity, build, run_both
 
 pytestmark = pytest.mark.gpu
 
@@ -69,3 +69,57 @@ def test_random_configuration_bit_exact(case):
     assert_parity(reader, out, expected, tokens, screened=screened)
     if padding is not None:
         assert not out[padding.to(out.device)].float().abs().sum()
+
+
+WIDE_CASES = 24
+
+
+def draw_wide(case: int) -> dict:
+    """A wide-layer case: the benchmark-scale shapes, skewed sizes and modes."""
+    rng = np.random.default_rng(19000 + case)
+    hidden = int(rng.choice([2048, 2816, 4096]))
+    width = int(rng.choice([512, 768, 1024, 1536, 2048]))
+    top_k = int(rng.choice([4, 6, 8, 10, 16]))
+    while top_k * width > 16384:
+        top_k //= 2
+    experts = int(rng.choice([16, 64, 128, 256]))
+    while experts > top_k and experts * 2 * width * hidden > 1.0e8:
+        experts //= 2
+    experts = max(experts, top_k)
+    tokens = int(rng.choice([1, 4, 16, 48, 128]))
+    while tokens * top_k > 8192:
+        tokens //= 2
+    mode = str(rng.choice(["top", "top", "top", "top", "threshold", "dense"]))
+    return {
+        "hidden": hidden, "width": width, "experts": experts, "top_k": top_k,
+        "rank": int(rng.choice([16, 32, 64])), "tokens": tokens, "mode": mode,
+        "retention": 1.0 if mode == "dense" else float(rng.choice([0.06, 0.123, 0.25])),
+        "keep": 1.0 if mode == "dense" else float(rng.choice([0.625, 1.0])),
+        "score": str(rng.choice(["point", "recovery-aware"])) if mode != "threshold" else "point",
+        "padded": [bool(p) for p in rng.random(tokens) < 0.1],
+    }
+
+
+@pytest.mark.parametrize("case", range(WIDE_CASES))
+def test_random_wide_configuration_bit_exact(case):
+    c = draw_wide(case)
+    print(f"wide case {case}: {c}", flush=True)
+    tokens = c["tokens"]
+    layer = make_routed_layer(hidden=c["hidden"], width=c["width"], experts=c["experts"],
+                              top_k=c["top_k"], rank=c["rank"], tokens=tokens, seed=900 + case)
+    plan = compile_budget(hidden_size=c["hidden"], expert_width=c["width"], top_k=c["top_k"],
+                          retention=c["retention"], screen_keep=c["keep"])
+    padding = torch.tensor(c["padded"]) if any(c["padded"]) else None
+    threshold = None
+    if c["mode"] == "threshold":
+        # a threshold that keeps about a tenth of the first token's candidates
+        probe = build(layer, plan, tokens, selection_score="point")
+        probe(layer.hidden.to(DEVICE), layer.ids.to(DEVICE), layer.weights.to(DEVICE))
+        ranked = probe.scores[0][0].sort(descending=True).values
+        threshold = float(ranked[plan.candidate_count // 10])
+        del probe
+    reader = build(layer, plan, tokens, selection_score=c["score"],
+                   selection_threshold=threshold)
+    out, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights, padding,
+                             threshold=threshold)
+    assert_parity(reader, out, expected, tokens, screened=c["mode"] != "dense")
