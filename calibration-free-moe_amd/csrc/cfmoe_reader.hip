@@ -2448,10 +2448,11 @@ constexpr int kGroupExactWaves = 1;
 constexpr int kExactChannels = 2;  // channels of one tile per grouped exact wave, in turn
 
 // The grouped exact launch's workgroups that are not (tile, channel) work:
-// the first kDownBuilders build the down order, those past the tile items run
-// recovery encoder items, then one per token writes the zero results of a
-// padded token or of slots with no local expert. Returns the tile item index
-// of a work workgroup, or -1 when the workgroup's part is done.
+// the first kDownBuilders build the down order, those past the routing's
+// tile items run recovery encoder items, then one per token writes the zero
+// results of a padded token or of slots with no local expert, and the rest
+// (the grid's tile items past the tile count) have nothing to do. Returns
+// the tile item index of a work workgroup, or -1 when its part is done.
 __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, int threads) {
   int block = blockIdx.x;
   if (a.down_order) {
@@ -2468,8 +2469,12 @@ __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, i
     }
     block -= kUnionCounters;
   }
-  if (block < a.tile_items) return block;
-  const int item = block - a.tile_items;
+  // the items of the routing's tiles come first, then the encoder and token
+  // items, then the tile items past the tile count (nothing to do): the
+  // encoder items are not dispatched behind the empty ones
+  const int live_items = min(load_uniform(a.group_total) * a.channel_groups, a.tile_items);
+  if (block < live_items) return block;
+  const int item = block - live_items;
   const int encode_blocks = (a.encode_items + 1) / 2;
   if (item < encode_blocks) {
     // two recovery encoder items (tile, slot, token), tile fastest; they read
@@ -2478,7 +2483,7 @@ __device__ __forceinline__ int group_exact_side_items(const GroupExactArgs &a, i
     return -1;
   }
   const int t = item - encode_blocks;
-  if (t >= a.T) return -1;
+  if (t >= a.T) return -1;  // (and the tile items past the tile count)
   const bool active = is_active(a.padding, t);
   for (int k = 0; k < a.K; ++k) {
     if (active && a.ids[t * a.K + k] >= 0) continue;
