@@ -1468,6 +1468,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void small_screen_kernel(SmallScr
 
 constexpr int kFusedWaves = 4;
 constexpr int kFusedThreads = 64 * kFusedWaves;
+// FP16 scale entries of a block: gate and up, each wave's row tile, four
+// entries of four rows each
+constexpr int kScaleQuads = kRowTile / 4;
+constexpr int kScaleBlock = 2 * kFusedWaves * kScaleQuads;
 // Tokens from which the fused screen runs: the per-channel-tile workgroups of
 // small_screen_kernel do a whole tile's work for each one-pair tile, so from
 // two tokens the fused screen is faster (Qwen3 layer: 13.0 against 17.2 us at
@@ -1503,10 +1507,10 @@ struct FusedScreenArgs {
 template <bool kGh5, int kSpan>
 struct FusedShared {
   alignas(16) int8_t digits[kStageBuffers][kSpan][3][kPairTile][kDigitStride];
-  // the split's FP16 scales (and residual scales) of the workgroup's four
-  // gate and four up row tiles: entry 32 kSpan kind + 32 bl + 16 up + 4 w + q
-  // holds rows 4q .. 4q + 3 of wave w's row tile
-  uint2 scales[kStageBuffers][(kGh5 ? 2 : 1) * kSpan * 32];
+  // the split's FP16 scales (and residual scales) of the workgroup's gate and
+  // up row tiles (one of each per wave): entry kScaleBlock (kSpan kind + bl)
+  // + 4 kFusedWaves up + 4 w + q holds rows 4q .. 4q + 3 of wave w's row tile
+  uint2 scales[kStageBuffers][(kGh5 ? 2 : 1) * kSpan * kScaleBlock];
   int qsum[kSpan * kMaxSplits][kPairTile];  // blocks x pairs
   int shift[kSpan * kMaxSplits][kPairTile];
   float norm2[kGh5 ? kSpan * kMaxSplits : 1][kPairTile];
@@ -1576,8 +1580,8 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   // thread tid's (block, pair) entries: tid = 16 b + p, then 16 (b + 16) + p
   // at span 4 (up to 32 blocks); loaded with the first split's staging,
   // stored after it
-  constexpr int kTableRounds = kSpan * kMaxSplits * kPairTile / kFusedThreads;
-  static_assert(kTableRounds * kFusedThreads == kSpan * kMaxSplits * kPairTile, "table rounds");
+  constexpr int kTableBlocks = kSpan * kMaxSplits;
+  constexpr int kTableRounds = (kTableBlocks * kPairTile + kFusedThreads - 1) / kFusedThreads;
   const int tp = tid % kPairTile;
   int qsum_value[kTableRounds], shift_value[kTableRounds];
   float norm2_value[kTableRounds];
@@ -1607,12 +1611,14 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
   // the last one). Lane offsets are fixed; per split the entries come through
   // a buffer resource over the split's blocks to the expert's last, so an
   // entry of a block past the expert (never used) reads zeros
-  constexpr int kScaleEntries = (kGh5 ? 2 : 1) * kSpan * 32;
+  constexpr int kScaleEntries = (kGh5 ? 2 : 1) * kSpan * kScaleBlock;
   static_assert(kScaleEntries <= kFusedThreads, "one scale entry per thread at most");
   const int sentry = tid % kScaleEntries;
-  const int sk = kGh5 ? sentry / (32 * kSpan) : 0, sbl = (sentry / 32) % kSpan, sup = (tid >> 4) & 1;
-  const int stile = (sup ? CT : 0) + min(group * kFusedWaves + ((tid >> 2) & 3), CT - 1);
-  const int srow = (sk ? 2 * a.I : 0) + kRowTile * stile + 4 * (tid & 3);
+  const int sk = kGh5 ? sentry / (kScaleBlock * kSpan) : 0, sbl = (sentry / kScaleBlock) % kSpan;
+  const int within = sentry % kScaleBlock;
+  const int sup = within / (kFusedWaves * kScaleQuads), sw = (within / kScaleQuads) % kFusedWaves;
+  const int stile = (sup ? CT : 0) + min(group * kFusedWaves + sw, CT - 1);
+  const int srow = (sk ? 2 * a.I : 0) + kRowTile * stile + 4 * (within % kScaleQuads);
   const int scale_offset = (sbl * 4 * a.I + srow) * 2;
   // each staging item's byte offset without its block term (fixed per thread)
   int stage_offset[kStagePerThread];
@@ -1656,6 +1662,7 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
     const int tb = tid / kPairTile + r * (kFusedThreads / kPairTile);
     // (stored negated: the block's chain starts from -qsum and scales by
     // 2^-shift)
+    if (kTableRounds * (kFusedThreads / kPairTile) > kTableBlocks && tb >= kTableBlocks) continue;
     sh.qsum[tb][tp] = table_live[r] ? -qsum_value[r] : 0;
     sh.shift[tb][tp] = table_live[r] ? -shift_value[r] : 0;
     if (kGh5) sh.norm2[kGh5 ? tb : 0][tp] = table_live[r] ? norm2_value[r] : 0.0f;
@@ -1702,9 +1709,9 @@ __global__ __launch_bounds__(kFusedThreads) __attribute__((amdgpu_waves_per_eu(k
       digit_dots(a0, a1, start, operand, acc);
 #pragma unroll
       for (int up = 0; up < 2; ++up) {
-        const int entry = 32 * bl + 16 * up + 4 * wave + (lane >> 4);
+        const int entry = kScaleBlock * bl + kFusedWaves * kScaleQuads * up + kScaleQuads * wave + (lane >> 4);
         const uint2 scale = sh.scales[buffer][entry];
-        const uint2 residual = kGh5 ? sh.scales[buffer][32 * kSpan + entry] : make_uint2(0u, 0u);
+        const uint2 residual = kGh5 ? sh.scales[buffer][kScaleBlock * kSpan + entry] : make_uint2(0u, 0u);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int sum = acc[up][r];
