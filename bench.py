@@ -158,6 +158,7 @@ STAGE_KERNELS = {"prepare": "prepare_kernel", "screen": "small_screen_kernel",
                  "select": "select_kernel", "exact": "exact_kernel",
                  "encode": "encode_kernel", "down": "down_kernel", "output": "output_kernel"}
 GROUP_EXACT_TOKENS = GROUPED_TOKENS  # batches from which the exact stage runs group_exact_kernel
+WIDE_OUTPUT_TOKENS = 64  # batches from which the output stage runs output_wide_kernel (top-k <= 16)
 
 
 def encoder_in_exact(tokens: int, rank: int) -> bool:
@@ -183,6 +184,8 @@ def stage_kernel(stage: str, tokens: int) -> str:
         return "group_exact_kernel"
     if stage == "screen" and tokens >= _ext.FUSED_SCREEN_TOKENS:
         return "fused_screen_kernel"
+    if stage == "output" and tokens >= WIDE_OUTPUT_TOKENS:
+        return "output_wide_kernel"
     return STAGE_KERNELS[stage]
 
 

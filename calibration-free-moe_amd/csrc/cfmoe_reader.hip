@@ -3927,7 +3927,11 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   const dim3 grid((s.H + op.columns - 1) / op.columns, tokens);
   const bool stageable = s.H % op.columns == 0 && s.K * s.R <= kOutputThreads &&
                          s.encoder_tiles <= kMaxEncoderTiles && rounds <= kStagedRoundsMax;
-  if (op.columns == 512)
+  // the two-round-trip kernel (slot records, encoder tiles and decoder row;
+  // then every item's tile partials at once) for 512 columns, and for 256
+  // from 64 tokens (c2's layer 160.5 -> 159.5 us; at 16 and 32 tokens it
+  // measured 0.4-0.6 us slower than the one-pass kernel)
+  if (op.columns == 512 || (op.columns == 256 && tokens >= 64))
     hipLaunchKernelGGL(output_wide_kernel, grid, dim3(kOutputThreads), value_lds, stream, op);
   else if (stageable && rounds <= 4)
     hipLaunchKernelGGL(output_staged_kernel<4>, grid, dim3(kOutputThreads), staged_lds, stream, op);
