@@ -399,11 +399,12 @@ constexpr int kGroupPairs = 16;    // pairs per screen tile (one MFMA column blo
 constexpr int kMaxExperts = 4096;  // local experts the grouping counts in LDS
 // Prepare workgroups: 256 threads, or 1024 from kWidePreparePairs routed
 // pairs (the routing workgroup, alone on its CU, is the launch's longest: at
-// 2048 pairs 1024 threads take it from 16.8 to 11.7 us; below 1024 pairs the
-// narrower cell workgroups spread the rotations over more CUs).
+// 2048 pairs 1024 threads take it from 16.8 to 11.7 us, at 512 pairs from
+// 8.7 to 8.3 us inside the layer; at 256 pairs the narrower cell workgroups,
+// spread over more CUs, win).
 constexpr int kPrepareThreads = 256;
 constexpr int kWidePrepareThreads = 1024;
-constexpr int kWidePreparePairs = 1024;
+constexpr int kWidePreparePairs = 512;
 
 // LDS of the routing block, carved from the launch's dynamic LDS, which the
 // host sizes for the call's pairs and experts (route_lds_bytes): the pairs'
@@ -3917,9 +3918,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   op.max_tiles = s.max_tiles;
   op.encoder_tiles = s.encoder_tiles;
   // wider workgroups fold each token's encoder tiles fewer times: 512 outputs
-  // from 128 tokens (c3 at 128 tokens: 18.4 -> 14.6 us), 256 from the grouped
-  // size, 64 below it; LDS K x columns x 4 <= 16 KB
-  op.columns = !grouped ? 64 : s.K <= 8 && tokens >= 128 ? 512 : s.K <= 16 ? 256 : 64;
+  // from 64 tokens (c3 at 128 tokens: 18.4 -> 14.6 us; at 100 tokens 13.7 ->
+  // 10.0, the launch's workgroups then fit at two per CU), 256 from the
+  // grouped size, 64 below it; LDS K x columns x 4 <= 16 KB
+  op.columns = !grouped ? 64 : s.K <= 8 && tokens >= 64 ? 512 : s.K <= 16 ? 256 : 64;
   const unsigned value_lds = static_cast<unsigned>(s.K * op.columns * sizeof(float));
   const long staged = static_cast<long>(s.max_tiles) * op.columns;  // partials per workgroup
   const long rounds = (staged + kOutputThreads - 1) / kOutputThreads;
@@ -3928,10 +3930,10 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   const bool stageable = s.H % op.columns == 0 && s.K * s.R <= kOutputThreads &&
                          s.encoder_tiles <= kMaxEncoderTiles && rounds <= kStagedRoundsMax;
   // the two-round-trip kernel (slot records, encoder tiles and decoder row;
-  // then every item's tile partials at once) for 512 columns, and for 256
-  // from 64 tokens (c2's layer 160.5 -> 159.5 us; at 16 and 32 tokens it
-  // measured 0.4-0.6 us slower than the one-pass kernel)
-  if (op.columns == 512 || (op.columns == 256 && tokens >= 64))
+  // then every item's tile partials at once) from 64 tokens, at 512 columns
+  // or, above top-8, 256 (c2's layer 160.9 -> 159.3 us; at 16 and 32 tokens
+  // it measured 0.4-0.6 us slower than the one-pass kernel)
+  if (tokens >= 64 && op.columns >= 256)
     hipLaunchKernelGGL(output_wide_kernel, grid, dim3(kOutputThreads), value_lds, stream, op);
   else if (stageable && rounds <= 4)
     hipLaunchKernelGGL(output_staged_kernel<4>, grid, dim3(kOutputThreads), staged_lds, stream, op);
