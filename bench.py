@@ -536,7 +536,7 @@ def summarize_trace(directory: str, command: str) -> str:
     durations: dict[str, list[int]] = {}
     reader_kernels = set(STAGE_KERNELS.values()) | {"select_all_kernel", "group_exact_kernel",
                                                      "fused_screen_kernel", "output_wide_kernel",
-                                                     "output_staged_kernel"}
+                                                     "output_staged_kernel", "select_exact_kernel"}
     for row in _rocprof_rows(directory, "kernel_trace.csv"):
         name = _short_name(row["Kernel_Name"])
         if name not in reader_kernels:

@@ -1782,6 +1782,7 @@ struct SelectArgs {
 
 constexpr int kSelectThreads = 1024;
 constexpr int kSelectKeys = 16;  // keys per thread: N <= 16384
+constexpr int kSelectExactTokens = 4;  // select and exact in one launch up to this batch
 
 // Histogram slot of a radix bin: one pad word per 32 bins, so that lanes
 // reading bins 32 apart use different LDS banks.
@@ -1857,8 +1858,16 @@ __device__ __forceinline__ int select_wide(const int *histogram, int *totals, in
                         count);
 }
 
+// The selection of token t by one workgroup of kSelectThreads threads (every
+// thread calls it; `write` is the same for the whole workgroup). Leaves the
+// thread's kept bits (bit j: candidate tid * per + j) in *kept_out and the
+// kept count before the thread in *base_out. With `write` it also stores the
+// outputs: kept ids, selected flags, completed flags (zeros, or with
+// `completed_kept` the selected flags, which the exact rows of a launch that
+// also runs them set anyway), slot records and tile mask bits.
 template <int kKeys>  // keys per thread: N <= kKeys * kSelectThreads
-__global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
+__device__ __forceinline__ void select_token(const SelectArgs &a, int t, bool write, bool completed_kept,
+                                             uint32_t *kept_out, int *base_out) {
   __shared__ int wide[2][kSelectWideSlots];
   __shared__ int last[kSelectLastSlots];
   __shared__ int scratch[32];
@@ -1866,7 +1875,7 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   __shared__ int wave_totals[kSelectWaves];
   __shared__ int slot_start[65];
   __shared__ int slot_tiles[64];
-  const int t = blockIdx.x, tid = threadIdx.x;
+  const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   if (a.tile_masks && tid < a.K) slot_tiles[tid] = a.pair_tiles[t * a.K + tid];
   for (int i = tid; i < 2 * kSelectWideSlots; i += kSelectThreads) (&wide[0][0])[i] = 0;
@@ -1994,6 +2003,9 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
   }
   const uint32_t kept_bits = above_bits | kept_tied;  // bit j: candidate first + j kept
   const int base = above_before + min(tied_before, room);
+  *kept_out = kept_bits;
+  *base_out = base;
+  if (!write) return;
   auto kept_below = [&](int j) { return __builtin_popcount(kept_bits & ((1u << j) - 1u)); };
   // a slot's first candidate in the thread's run (at most one: I >= the run):
   // the kept ids before it start the slot
@@ -2013,8 +2025,8 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
                  1u << (slot_tile % kGroupPairs));
     }
   }
-  // the run's selected flags (and cleared completed flags) as one store per
-  // 4 or 2 candidates where the run allows
+  // the run's selected flags (and completed flags: cleared, or the selected
+  // ones) as one store per 4 or 2 candidates where the run allows
   {
     uint8_t *selected = a.selected + static_cast<long>(t) * a.N + first;
     uint8_t *completed = a.completed + static_cast<long>(t) * a.N + first;
@@ -2023,23 +2035,24 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
 #pragma unroll
       for (int j = 0; j < kKeys; j += 4)
         if (j < per && first + j < a.N) {
-          *reinterpret_cast<uint32_t *>(selected + j) =
-              flag(j) | flag(j + 1) << 8 | flag(j + 2) << 16 | flag(j + 3) << 24;
-          *reinterpret_cast<uint32_t *>(completed + j) = 0u;
+          const uint32_t flags = flag(j) | flag(j + 1) << 8 | flag(j + 2) << 16 | flag(j + 3) << 24;
+          *reinterpret_cast<uint32_t *>(selected + j) = flags;
+          *reinterpret_cast<uint32_t *>(completed + j) = completed_kept ? flags : 0u;
         }
     } else if (per % 2 == 0) {
 #pragma unroll
       for (int j = 0; j < kKeys; j += 2)
         if (j < per && first + j < a.N) {
-          *reinterpret_cast<uint16_t *>(selected + j) = static_cast<uint16_t>(flag(j) | flag(j + 1) << 8);
-          *reinterpret_cast<uint16_t *>(completed + j) = 0;
+          const uint16_t flags = static_cast<uint16_t>(flag(j) | flag(j + 1) << 8);
+          *reinterpret_cast<uint16_t *>(selected + j) = flags;
+          *reinterpret_cast<uint16_t *>(completed + j) = completed_kept ? flags : 0;
         }
     } else {
 #pragma unroll
       for (int j = 0; j < kKeys; ++j)
         if (j < per && first + j < a.N) {
           selected[j] = static_cast<uint8_t>(flag(j));
-          completed[j] = 0;
+          completed[j] = completed_kept ? static_cast<uint8_t>(flag(j)) : 0;
         }
     }
   }
@@ -2061,6 +2074,13 @@ __global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
       a.down_tile_starts[t * a.K + tid] = tile16;
     }
   }
+}
+
+template <int kKeys>
+__global__ __launch_bounds__(kSelectThreads) void select_kernel(SelectArgs a) {
+  uint32_t kept;
+  int base;
+  select_token<kKeys>(a, blockIdx.x, true, false, &kept, &base);
 }
 
 // Full retention: every candidate is kept (progressive.py:2999-3004).
@@ -2177,12 +2197,28 @@ __global__ __launch_bounds__(64) void encode_kernel(EncodeArgs a) {
 // from where every step reads four values of its half's item at once
 // (broadcast reads). The coefficients E[c][r] arrive packed two to a word.
 // Same order and roundings as encode_tile.
+//
+// The selected and completed flags come from the workspace (one-wave
+// workgroups, whose LDS values array is the function's own), or, in a
+// workgroup of several waves that ran the token's selection itself
+// (KeptBits), the selected flags from that selection's kept bits and no
+// completed flag (a skipped channel is never completed), the values through
+// the wave's own LDS rows `staged`.
 constexpr int kDirectRank = 32;
 
-template <class Args>  // EncodeArgs, or the grouped exact launch's arguments
-__device__ __forceinline__ void encode_pair_direct(const Args &a, int p, int items, int t_base) {
+struct WorkspaceFlags {};
+struct KeptBits {
+  const uint32_t *bits;  // thread j's kept bits: bit i is candidate j per + i of the token
+  int per;
+};
+
+template <class Args, class Flags = WorkspaceFlags>  // Args: EncodeArgs or the grouped exact launch's
+__device__ __forceinline__ void encode_pair_direct(const Args &a, int p, int items, int t_base,
+                                                   Flags flags = Flags(), float (*staged)[64] = nullptr) {
   constexpr int R = kDirectRank;
-  __shared__ __align__(16) float channel_values[2][64];
+  constexpr bool kFromBits = std::is_same<Flags, KeptBits>::value;
+  __shared__ __align__(16) float own_values[kFromBits ? 1 : 2][64];
+  float (*channel_values)[64] = kFromBits ? staged : own_values;
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, r = lane & 31;
   const int q = min(2 * p + h, items - 1);
@@ -2204,8 +2240,14 @@ __device__ __forceinline__ void encode_pair_direct(const Args &a, int p, int ite
     const int j = 32 * s + r;
     const bool inside = tile * 64 + j < a.I;
     const long at = inside ? j : 0;
-    is_selected[s] = inside ? a.selected[flat + at] : 1;
-    is_completed[s] = a.completed[flat + at];
+    if constexpr (kFromBits) {
+      const int i = k * a.I + tile * 64 + static_cast<int>(at);
+      is_selected[s] = inside ? (flags.bits[i / flags.per] >> (i % flags.per)) & 1u : 1;
+      is_completed[s] = 0;
+    } else {
+      is_selected[s] = inside ? a.selected[flat + at] : 1;
+      is_completed[s] = a.completed[flat + at];
+    }
     exact[s] = a.activations[flat + at];
     gate[s] = a.partial[base + at];
     up[s] = a.partial[base + a.N + at];
@@ -2234,7 +2276,15 @@ __device__ __forceinline__ void encode_pair_direct(const Args &a, int p, int ite
       value = is_completed[s] ? bf16f(exact[s]) : bfr(cfm_activate(bfr(gate[s]), a.gelu != 0) * bfr(up[s]));
     channel_values[h][32 * s + r] = value;
   }
-  __syncthreads();  // one-wave workgroups: orders the LDS writes before the reads
+  if constexpr (kFromBits) {
+    // the wave's own rows: its LDS writes before its reads (in order within
+    // a wave; the fences keep the compiler from moving them)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  } else {
+    __syncthreads();  // one-wave workgroups: orders the LDS writes before the reads
+  }
   const float4 *values = reinterpret_cast<const float4 *>(channel_values[h]);
   float acc = 0.0f;
 #pragma unroll
@@ -2794,32 +2844,15 @@ struct ExactArgs {
   int padding_bytes;
 };
 
-// Workgroup = one wave = kept channel f of token t: single-wave workgroups
-// spread a batch-1 call's rows over every CU. The kept id, the token's expert
-// ids and its padding flag arrive in one round trip, then the gate, up and
+// Kept channel `logical` of token t on one wave (lane k < K holds slot k's
+// expert in slot_id, `padded` the token's padding flag): the gate, up and
 // hidden rows with every part in flight (buffer resources: parts past H, and
-// a padded token's hidden row, read zeros); the chain is row_dots, as in
-// group_exact_kernel.
+// a padded token's hidden row, read zeros), the chain row_dots as in
+// group_exact_kernel, then lane 0 stores the results.
 template <int kParts>
-__global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
-  const int lane = threadIdx.x;
-  const int t = blockIdx.y;
-  if (static_cast<int>(blockIdx.x) >= a.exact_blocks) {
-    const int item = blockIdx.x - a.exact_blocks;  // (tile, slot), tile fastest
-    if (2 * item < a.encode_items) encode_pair_direct(a.encode, item, a.encode_items, t);
-    return;
-  }
-  const int f = blockIdx.x;
-  asm volatile("" ::"s"(a.partial), "s"(a.activations), "s"(a.completed), "s"(a.gate_up), "s"(a.x),
-               "s"(a.H), "s"(a.I), "s"(a.N), "s"(a.gelu), "s"(a.ids), "s"(a.next_ids), "s"(a.K),
-               "s"(a.F), "s"(a.padding_source), "s"(a.padding_bytes));
-  const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
-  const uint32_t padded =
-      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.padding_source, a.padding_bytes), t, 0, 0);
-  const int logical =
-      __builtin_amdgcn_readfirstlane(load_global(a.next_ids + static_cast<long>(t) * a.F + f));
-  asm volatile("" ::"v"(padded));  // the flag's load stays in this round trip
-  if (logical < 0 || logical >= a.N) return;
+__device__ __forceinline__ void exact_channel(const ExactArgs &a, int t, int logical, int slot_id,
+                                              uint32_t padded) {
+  const int lane = threadIdx.x & 63;
   const int k = logical / a.I, c = logical % a.I;
   const int e = __builtin_amdgcn_readlane(slot_id, k);
   float g = 0.0f, u = 0.0f;
@@ -2857,6 +2890,89 @@ __global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
     a.completed[static_cast<long>(t) * a.N + logical] = 1;
   }
 }
+
+// Workgroup = one wave = kept channel f of token t: single-wave workgroups
+// spread a batch-1 call's rows over every CU. The kept id, the token's expert
+// ids and its padding flag arrive in one round trip, then the gate, up and
+// hidden rows with every part in flight (buffer resources: parts past H, and
+// a padded token's hidden row, read zeros); the chain is row_dots, as in
+// group_exact_kernel.
+template <int kParts>
+__global__ __launch_bounds__(64) void exact_kernel(ExactArgs a) {
+  const int lane = threadIdx.x;
+  const int t = blockIdx.y;
+  if (static_cast<int>(blockIdx.x) >= a.exact_blocks) {
+    const int item = blockIdx.x - a.exact_blocks;  // (tile, slot), tile fastest
+    if (2 * item < a.encode_items) encode_pair_direct(a.encode, item, a.encode_items, t);
+    return;
+  }
+  const int f = blockIdx.x;
+  asm volatile("" ::"s"(a.partial), "s"(a.activations), "s"(a.completed), "s"(a.gate_up), "s"(a.x),
+               "s"(a.H), "s"(a.I), "s"(a.N), "s"(a.gelu), "s"(a.ids), "s"(a.next_ids), "s"(a.K),
+               "s"(a.F), "s"(a.padding_source), "s"(a.padding_bytes));
+  const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
+  const uint32_t padded =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.padding_source, a.padding_bytes), t, 0, 0);
+  const int logical =
+      __builtin_amdgcn_readfirstlane(load_global(a.next_ids + static_cast<long>(t) * a.F + f));
+  asm volatile("" ::"v"(padded));  // the flag's load stays in this round trip
+  if (logical < 0 || logical >= a.N) return;
+  exact_channel<kParts>(a, t, logical, slot_id, padded);
+}
+
+// Select and exact in one launch for the smallest batches (no kernel boundary
+// and no kept-id round trip between them). Workgroup (g, token t) of
+// kSelectThreads threads runs the token's selection (select_token: the same
+// keys, passes and scans in every workgroup, so all find the same kept
+// ids); workgroup 0 stores the select outputs, and wave w < item_waves of
+// workgroup g > 0 takes item q = item_waves (g - 1) + w: the q-th kept
+// channel (q < F), found from the threads' kept bits and inclusive kept counts
+// in LDS, or past F the recovery encoder pair item q - F, whose selected
+// flags come from the same bits. The slot experts and padding flag are loaded
+// before the selection. The host sizes item_waves so that the workgroups
+// (one per compute unit at 16 waves of this kernel's registers) run in one
+// round: the rows then come through as many compute units as that allows.
+template <int kKeys, int kParts>
+__global__ __launch_bounds__(kSelectThreads) void select_exact_kernel(SelectArgs s, ExactArgs a,
+                                                                      int item_waves) {
+  __shared__ int kept_end[kSelectThreads];
+  __shared__ uint32_t kept_bits[kSelectThreads];
+  __shared__ __align__(16) float values[kSelectWaves][2][64];
+  const int t = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool writer = blockIdx.x == 0;
+  const int slot_id = lane < a.K ? load_global(a.ids + t * a.K + lane) : -1;
+  const uint32_t padded =
+      __builtin_amdgcn_raw_buffer_load_b8(buffer_resource(a.padding_source, a.padding_bytes), t, 0, 0);
+  uint32_t kept;
+  int base;
+  select_token<kKeys>(s, t, writer, true, &kept, &base);
+  if (writer) return;
+  kept_end[tid] = base + __builtin_popcount(kept);
+  kept_bits[tid] = kept;
+  __syncthreads();
+  if (wave >= item_waves) return;
+  const int per = (s.N + kSelectThreads - 1) / kSelectThreads;
+  const int q = (static_cast<int>(blockIdx.x) - 1) * item_waves + wave;
+  if (q < a.F) {
+    // the thread j whose kept run holds position q: lane l reads the end of
+    // threads 16 l .. 16 l + 15, then lane l < 16 thread 16 c + l's
+    const int chunk_end = kept_end[16 * lane + 15];
+    const uint64_t past = __ballot(chunk_end > q);
+    if (!past) return;  // q is at or past the kept count: no channel
+    const int c = __builtin_ctzll(past);
+    const int end = lane < 16 ? kept_end[16 * c + lane] : 0;
+    const int j = 16 * c + __builtin_ctzll(__ballot(lane < 16 && end > q));
+    const int before = j > 0 ? kept_end[j - 1] : 0;
+    uint32_t bits = kept_bits[j];
+    for (int n = q - before; n > 0; --n) bits &= bits - 1;
+    const int logical = __builtin_amdgcn_readfirstlane(j * per + __builtin_ctz(bits));
+    exact_channel<kParts>(a, t, logical, slot_id, padded);
+  } else if (2 * (q - a.F) < a.encode_items) {
+    encode_pair_direct(a.encode, q - a.F, a.encode_items, t, KeptBits{kept_bits, per}, values[wave]);
+  }
+}
+
 
 // ---------------------------------------------------------------------------
 // output (progressive.py:1954-2111): latent, decoder correction, router mix
@@ -3659,6 +3775,15 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
   const bool masked = s.screened && grouped;
   sel.pair_tiles = workspace->pair_tiles;
   sel.tile_masks = masked ? workspace->tile_masks : nullptr;
+  // Up to kSelectExactTokens tokens a call that runs both stages runs select
+  // and exact as one launch (select_exact_kernel, in the exact launch's place)
+  // when its workgroups at 16 item waves each fit on the compute units at
+  // once (a second round would cost more than the launch saves)
+  const int fused_items = s.F + (s.R == kDirectRank ? (s.encoder_tiles * s.K + 1) / 2 : 0);
+  const bool fuse_select = s.screened && !grouped && tokens <= kSelectExactTokens &&
+                           (stages & (1u << CFMOE_STAGE_SELECT)) && (stages & (1u << CFMOE_STAGE_EXACT)) &&
+                           hidden_parts(s.H) == kNarrowParts &&
+                           tokens * (1L + (fused_items + kSelectWaves - 1) / kSelectWaves) <= compute_units();
 
   if (s.screened) {
     const uint2 *trit_planes = reinterpret_cast<const uint2 *>(weights->trit_planes);
@@ -3733,7 +3858,7 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
       if ((rc = check_launch("screen"))) return rc;
     }
 
-    if (stages & (1u << CFMOE_STAGE_SELECT)) {
+    if ((stages & (1u << CFMOE_STAGE_SELECT)) && !fuse_select) {
       if (s.N <= 8 * kSelectThreads)
         hipLaunchKernelGGL(select_kernel<8>, dim3(tokens), dim3(kSelectThreads), 0, stream, sel);
       else
@@ -3852,7 +3977,21 @@ static int run_stages(uint32_t stages, const cfmoe_dims *dims, const cfmoe_weigh
     ex.encode_items = encode_items;
     ex.padding_source = padding ? static_cast<const void *>(padding) : static_cast<const void *>(weights->signs);
     ex.padding_bytes = padding ? tokens : 0;
-    if (hidden_parts(s.H) == kNarrowParts)
+    if (fuse_select) {
+      // the fewest item waves per workgroup that fit the launch's workgroups
+      // (one per token writing, the rest taking items) on the compute units
+      const int items = s.F + (encode_items + 1) / 2;  // fused_items
+      const long groups = std::max(1L, compute_units() / tokens - 1);
+      const int item_waves =
+          static_cast<int>(std::min<long>(kSelectWaves, std::max<long>(1, (items + groups - 1) / groups)));
+      const dim3 grid(1 + (items + item_waves - 1) / item_waves, tokens);
+      if (s.N <= 8 * kSelectThreads)
+        hipLaunchKernelGGL((select_exact_kernel<8, kNarrowParts>), grid, dim3(kSelectThreads), 0, stream, sel, ex,
+                           item_waves);
+      else
+        hipLaunchKernelGGL((select_exact_kernel<kSelectKeys, kNarrowParts>), grid, dim3(kSelectThreads), 0, stream,
+                           sel, ex, item_waves);
+    } else if (hidden_parts(s.H) == kNarrowParts)
       hipLaunchKernelGGL(exact_kernel<kNarrowParts>, dim3(s.F + (encode_items + 1) / 2, tokens), dim3(kWave), 0,
                          stream, ex);
     else

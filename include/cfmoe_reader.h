@@ -167,7 +167,9 @@ CFMOE_API int cfmoe_forward(const cfmoe_dims *dims, const cfmoe_weights *weights
 /* Launch one stage of cfmoe_forward with the same arguments, reading the
  * workspace state that earlier stages left. For per-kernel timing and tests;
  * no reference counterpart (the reference launches its Triton kernels
- * individually from Python, progressive.py:3955-4471). */
+ * individually from Python, progressive.py:3955-4471). A stage launched alone
+ * runs its own kernel even where cfmoe_forward runs it in one launch with the
+ * next (select and exact up to four tokens); the results are the same. */
 CFMOE_API int cfmoe_launch_stage(int32_t stage, const cfmoe_dims *dims, const cfmoe_weights *weights,
                        const cfmoe_workspace *workspace, const void *hidden,
                        const void *router_ids, const void *router_weights,

@@ -4,6 +4,8 @@
   `reader(..., input_prepared=True)`, the order the reference's vLLM binding
   uses (runtime/experts.py:402-427, :497-505; progressive.py:3829-3873).
 * The default constructor, which builds the sketch itself (`sketch=None`).
+* Select and exact in one launch (up to four tokens) against the stages
+  relaunched one at a time, which run the separate kernels.
 * The configurations without a test elsewhere: Qwen3-30B-A3B at batch 128 and
   the 256-expert layer at batch 1, with point-only (keep 1.0) and two-stage
   (keep 0.625) screening.
@@ -15,6 +17,7 @@ import numpy as np
 import pytest
 import torch
 
+from calibration_free_moe.reader import _ext
 from calibration_free_moe.reader.budget import compile_budget
 from calibration_free_moe.reader.progressive import ProgressiveReader, channel_major_down
 from tests.synthetic import make_layer
@@ -112,6 +115,57 @@ def test_prepared_input_runs_on_the_side_stream(tokens):
     _, expected = run_both(reader, layer, plan, x.cpu(), layer.ids, layer.weights, padding.cpu())
     assert reader.prepare_input(x, padding)
     out = reader(x, ids, weights, padding, input_prepared=True)
+    torch.cuda.synchronize()
+    assert_parity(reader, out, expected, tokens)
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 4])
+@pytest.mark.parametrize("rank", [16, 32])
+def test_select_and_exact_in_one_launch_equal_the_stages(tokens, rank):
+    """Up to four tokens a full call runs select and exact as one launch: every
+    workgroup selects, one stores the selection, the others compute the kept
+    rows and (at rank 32) the recovery encoder items from their own copy of
+    it. The stages relaunched one at a time run the separate kernels. Both
+    leave the same outputs bit for bit, from stale flags too, and the call
+    matches the oracle."""
+    layer = make_layer(hidden=2048, width=768, experts=16, top_k=8, rank=rank, tokens=tokens,
+                       seed=120 + tokens + rank)
+    plan = compile_budget(hidden_size=2048, expert_width=768, top_k=8, retention=0.123,
+                          screen_keep=0.625)
+    reader = build(layer, plan, tokens, selection_score="point")
+    hidden = layer.hidden.to(DEVICE)
+    ids, weights = layer.ids.to(DEVICE), layer.weights.to(DEVICE)
+    padding = torch.zeros(tokens, dtype=torch.bool, device=DEVICE)
+    padding[-1] = tokens > 1
+    names = ("selected", "completed", "partial", "counts", "starts", "tile_starts", "latent")
+
+    def state():
+        got = {name: getattr(reader, name)[:tokens].clone() for name in names}
+        got["next_ids"] = reader.candidate_ids[-1][:tokens].clone()
+        kept = got["completed"].bool()
+        got["activations"] = torch.where(kept, reader.activations[:tokens], 0)
+        return got
+
+    out = reader(hidden, ids, weights, padding).clone()
+    torch.cuda.synchronize()
+    fused = state()
+    # stale selection state: the stages rewrite all of it
+    reader.selected.fill_(1)
+    reader.completed.fill_(1)
+    reader.candidate_ids[-1].fill_(-7)
+    staged = torch.empty_like(out)
+    for stage in _ext.STAGES:
+        reader.launch_stage(stage, hidden, ids, weights, padding, staged)
+    torch.cuda.synchronize()
+    assert torch.equal(staged, out)
+    for name, value in state().items():
+        assert torch.equal(value, fused[name]), name
+    # and the fused call again, from the same stale state
+    reader.selected.fill_(1)
+    reader.completed.fill_(1)
+    reader.candidate_ids[-1].fill_(-7)
+    _, expected = run_both(reader, layer, plan, layer.hidden, layer.ids, layer.weights, padding.cpu())
+    out = reader(hidden, ids, weights, padding)
     torch.cuda.synchronize()
     assert_parity(reader, out, expected, tokens)
 
