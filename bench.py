@@ -684,7 +684,9 @@ def main() -> int:
             "stage_us": "each stage relaunched alone (cfmoe_launch_stage) 4 times over the stack's "
                         "layers in one HIP graph, after one full call of the last layer: every "
                         "relaunch reads the workspace that call left (the score stage, and the "
-                        "encode stage at rank 32, launch nothing); timing only",
+                        "encode stage at rank 32, launch nothing; up to four tokens the layer "
+                        "runs select and exact as one launch, relaunched here as their separate "
+                        "kernels); timing only",
         },
         "us_per_layer_steps": round(headline["us_per_layer_steps"], 3),
         "us_per_layer_median_step": round(headline["us_per_layer_median_event"], 3),
