@@ -263,8 +263,8 @@ def time_graph(graph: torch.cuda.CUDAGraph, warmup: int, steps: int,
 
     After `warmup` untimed replays: (1) exactly `steps` replays, bracketed by
     synchronisations, give `ms_per_step` (their mean) and per-step event
-    times; (2) the measurement plan of BASELINE.md section 3 (the reference's
-    scripts/speed_block.py:379-414): a pilot of about `sample_seconds`
+    times; (2) the reference's measurement plan
+    (scripts/speed_block.py:379-414): a pilot of about `sample_seconds`
     (PILOT_SECONDS by default) sizes a sample of `replays` replays, and the
     median of PLAN_SAMPLES such samples (each bracketed by events on the
     graph's stream) is `ms_median`. Profiler runs pass a shorter sample, so the
@@ -678,7 +678,7 @@ def main() -> int:
         "timing": {
             "value": f"median of {PLAN_SAMPLES} samples after the {args.warmup} warm-up replays, each "
                      f"sample {headline['replays_per_sample']} graph replays sized by a pilot of "
-                     f"about {args.sample_seconds} s (BASELINE.md section 3; the reference's "
+                     f"about {args.sample_seconds} s (the reference's measurement plan, "
                      "scripts/speed_block.py:379-414), divided by the layers",
             "ms_per_step": f"mean of exactly {args.steps} replays between synchronisations",
             "stage_us": "each stage relaunched alone (cfmoe_launch_stage) 4 times over the stack's "
