@@ -1,11 +1,12 @@
 """Benchmark of the MI355X sparse expert reader (one JSON line on stdout).
 
-Workload (`--config`, default c2): the BASELINE configuration the metric is
+Workload (`--config`, default c2): the configuration the headline metric is
 quoted on that fits one GPU -- a stack of L distinct synthetic MoE layers
 (random-init BF16 weights, their ternary sketches and rank-32 recovery maps),
 each with its own decode batch of T tokens routed by a softmax router. One
 step replays a HIP graph holding the L reader calls on one stream; the reported
-value is microseconds per layer (mean over the timed steps).
+value is microseconds per layer (the median of the measurement plan's samples;
+`ms_per_step` is the mean of exactly the timed steps).
 
 Also reported: tokens/s, the algorithmic HBM bytes of each layer call (per
 expert touched: union of kept coordinates' code runs, FP16 scale plane and FP32
